@@ -1,0 +1,150 @@
+/*
+ * sps_attn.h - C ABI of the MI355X (gfx950) SPS attention hot path.
+ *
+ * One shared library (libsps_attn.so) exports the three kernel families of the SPS Transformer's
+ * attention path. All entry points are stateless, take plain device pointers, element strides and
+ * sizes, enqueue asynchronously on the caller's HIP stream (passed as void*, a hipStream_t), never
+ * synchronise the host and never allocate device memory: scratch space is a caller-provided
+ * workspace whose size the *_workspace_bytes functions report. They return SPS_OK or an error
+ * code; sps_last_error() returns the message of the calling thread's last failure.
+ *
+ * Tensor conventions. A [B, H, N, D] tensor is described by its base pointer and the element
+ * strides {b, h, n}; the D axis must be contiguous, the base 16-byte aligned and every stride a
+ * multiple of 8 elements (16 bytes). Document ids are a [B, N] int32 or int64 array with unit
+ * stride along N. Positions of the SPS families index the interleaved input/<predict> sequence
+ * (token t owns positions 2t and 2t+1), so N must be even there.
+ *
+ * Reference interfaces replaced (lil-lab/sps, paths under src/modeling/models/):
+ *   sps_attn_fwd / sps_attn_bwd   <- _sps_sliding_attention.forward/backward
+ *                                    (attention/triton_sps_flash_attention.py:491-722),
+ *                                    _reverse_sps_sliding_attention.forward/backward
+ *                                    (attention/triton_reverse_sps_flash_attention.py:602-824),
+ *                                    _full_attention.forward/backward
+ *                                    (attention/triton_full_flash_attention.py:463-676)
+ *   sps_decode                    <- triton_segmented_q1_attention (utils/decode_attention.py:393-480),
+ *                                    triton_segmented_q2_attention (utils/decode_attention.py:483-594)
+ *   sps_attn_mask                 <- the mask block of _attn_fwd_inner_sps
+ *                                    (attention/triton_sps_flash_attention.py:70-111); a
+ *                                    verification entry point that materialises the mask the
+ *                                    kernels evaluate.
+ */
+#ifndef SPS_ATTN_H
+#define SPS_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define SPS_OK 0
+#define SPS_E_INVALID 1     /* malformed argument (null pointer, bad shape, misaligned stride) */
+#define SPS_E_UNSUPPORTED 2 /* well-formed but outside this build (head dim, dtype) */
+#define SPS_E_WORKSPACE 3   /* workspace smaller than *_workspace_bytes reports */
+#define SPS_E_HIP 4         /* HIP runtime error while enqueueing */
+
+/* Element types. */
+#define SPS_DTYPE_BF16 0
+#define SPS_DTYPE_F16 1
+#define SPS_DTYPE_F32 2
+#define SPS_DTYPE_I32 3
+#define SPS_DTYPE_I64 4
+
+/* Attention families (mask semantics). */
+#define SPS_FAMILY_FULL 0        /* causal + document mask (full_attention) */
+#define SPS_FAMILY_SPS 1         /* persistent keys at even positions (sps_sliding_attention) */
+#define SPS_FAMILY_REVERSE_SPS 2 /* persistent keys at odd positions (reverse_sps_sliding_attention,
+                                    also used by the delayed-state model) */
+
+/* Version string of the library. */
+const char* sps_version(void);
+
+/* Copies the calling thread's last error message into buf (NUL-terminated, truncated to len)
+ * and returns the full message length. */
+int sps_last_error(char* buf, size_t len);
+
+/* Workspace needed by sps_attn_fwd (backward = 0), sps_attn_bwd (backward = 1) or
+ * sps_attn_mask (backward = 0). */
+size_t sps_attn_workspace_bytes(int family, int B, int H, int N, int has_docs, int backward);
+
+/*
+ * Forward attention. q, k, v, o: [B, H, N, D] of dtype (bf16 or f16), D in {16, 32, 64, 128}.
+ * lse: [B, H, N] fp32 contiguous, receives the log2-domain log-sum-exp of the scaled scores
+ * (m + log2 l), consumed by sps_attn_bwd. docs may be NULL (no document mask).
+ * window: temporary-key window in tokens (SPS families). has_pkw/pkw: optional persistent-key
+ * window (the reference's persistent_key_window; has_pkw = 0 means None). sm_scale must be > 0.
+ */
+int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype,
+                 const void* q, const int64_t* q_strides,
+                 const void* k, const int64_t* k_strides,
+                 const void* v, const int64_t* v_strides,
+                 void* o, const int64_t* o_strides,
+                 float* lse,
+                 const void* docs, int docs_dtype, int64_t docs_stride_b,
+                 float sm_scale, int window, int has_pkw, int pkw,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Backward attention: given dO, writes dq, dk, dv (same dtype as q). o and lse are the forward
+ * outputs. The workspace also holds rowsum(o * dO).
+ */
+int sps_attn_bwd(int family, int B, int H, int N, int D, int dtype,
+                 const void* q, const int64_t* q_strides,
+                 const void* k, const int64_t* k_strides,
+                 const void* v, const int64_t* v_strides,
+                 const void* o, const int64_t* o_strides,
+                 const void* dout, const int64_t* dout_strides,
+                 const float* lse,
+                 void* dq, const int64_t* dq_strides,
+                 void* dk, const int64_t* dk_strides,
+                 void* dv, const int64_t* dv_strides,
+                 const void* docs, int docs_dtype, int64_t docs_stride_b,
+                 float sm_scale, int window, int has_pkw, int pkw,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Writes into mask ([B, N, N] uint8, zero-filled by the caller) a 1 for every (query, key) pair
+ * that the attention kernels treat as visible, following the block schedule of the
+ * query-stationary kernels (schedule = 0: forward and dQ) or of the key-stationary dK/dV kernel
+ * (schedule = 1). Used to prove the kernels' masks bit-exact against the reference predicate.
+ */
+int sps_attn_mask(int family, int B, int N,
+                  const void* docs, int docs_dtype, int64_t docs_stride_b,
+                  int window, int has_pkw, int pkw, int schedule, uint8_t* mask,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace needed by sps_decode for the given segment scan lengths. */
+size_t sps_decode_workspace_bytes(int B, int H, int D, int nq, int kv_dtype, int n_seg,
+                                  const int64_t* seg_scan);
+
+/*
+ * Segmented decode attention, nq in {1, 2} queries per (batch, head).
+ * q: fp32 [B, nq, H, D] (values already rounded to the attention dtype), strides {b, slot, h}.
+ * Segments (n_seg <= 3): K and V [B, H, storage, D] of kv_dtype (bf16, f16 or f32) with strides
+ * {b, h, t}; live lengths seg_len[s] ([B] if seg_len_per_head[s] == 0, else [B, H]) of dtype
+ * SPS_DTYPE_I32 or SPS_DTYPE_I64; key t of segment s is attended iff
+ * t < min(max(len, 0), seg_scan[s]).
+ * Extras (n_extra <= 2): fp32 [B, H, D] keys/values sharing strides {b, h}; extra e is attended by
+ * query slot j iff bit j of extra_query_mask[e] is set (q=1: 1; q=2: current input 3, current
+ * <predict> 2). out: fp32 [B, nq, H, D], strides {b, slot, h}; 0 where nothing is attended.
+ * D in {16, 32, 64, 128, 256}.
+ */
+int sps_decode(int B, int H, int D, int nq,
+               const float* q, const int64_t* q_strides,
+               int kv_dtype, int n_seg,
+               const void* const* seg_k, const int64_t* seg_k_strides,
+               const void* const* seg_v, const int64_t* seg_v_strides,
+               const void* const* seg_len, const int* seg_len_dtype, const int* seg_len_per_head,
+               const int64_t* seg_scan,
+               int n_extra, const float* const* extra_k, const float* const* extra_v,
+               const int64_t* extra_strides, const int* extra_query_mask,
+               float sm_scale, float* out, const int64_t* out_strides,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPS_ATTN_H */

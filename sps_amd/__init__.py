@@ -1,0 +1,39 @@
+"""sps_amd: MI355X-native (gfx950) attention hot path of the SPS Transformer.
+
+Drop-in replacements for the reference's attention entry points:
+  prefill / training: ``sps_sliding_attention``, ``reverse_sps_sliding_attention``, ``full_attention``
+  decode:             ``KVSegment``, ``triton_segmented_q1_attention``, ``triton_segmented_q2_attention``,
+                      ``masked_kv_attention``
+  document ids:       ``generate_left_padded_document_idx``
+All compute runs in libsps_attn.so (hand-written HIP kernels); see include/sps_attn.h.
+"""
+
+from .attention import full_attention, reverse_sps_sliding_attention, sps_sliding_attention
+from .decode_attention import (
+    KVSegment,
+    masked_kv_attention,
+    triton_segmented_q1_attention,
+    triton_segmented_q2_attention,
+)
+from .document_idx import (
+    compute_left_padded_position_ids,
+    generate_left_padded_document_idx,
+    infer_is_real_tokens,
+    validate_left_padded_tokens,
+)
+from .integration import install_into_modeling
+
+__all__ = [
+    "sps_sliding_attention",
+    "reverse_sps_sliding_attention",
+    "full_attention",
+    "KVSegment",
+    "triton_segmented_q1_attention",
+    "triton_segmented_q2_attention",
+    "masked_kv_attention",
+    "generate_left_padded_document_idx",
+    "compute_left_padded_position_ids",
+    "infer_is_real_tokens",
+    "validate_left_padded_tokens",
+    "install_into_modeling",
+]

@@ -1,0 +1,260 @@
+"""Drop-in prefill/training attention for the SPS model families, backed by libsps_attn.so.
+
+Public functions keep the reference names, signatures, argument meaning and assertion behaviour:
+
+* ``sps_sliding_attention``          <- attention/triton_sps_flash_attention.py:725-753
+* ``reverse_sps_sliding_attention``  <- attention/triton_reverse_sps_flash_attention.py:827-853
+* ``full_attention``                 <- attention/triton_full_flash_attention.py:679-709
+
+(paths relative to src/modeling/models/ of lil-lab/sps). Differences that do not change results:
+no padding of N to a multiple of 128 (the kernels bounds-check), no ``.contiguous()`` copies of
+[B, N, H, D]-strided views (the kernels take element strides), and the output is allocated in
+[B, N, H, D] memory order so the caller's ``y.transpose(1, 2).contiguous()`` is free.
+``warp_specialize`` is accepted and ignored (it selects a Triton code path in the reference).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _native as N
+
+_SUPPORTED_HEAD_DIMS = (16, 32, 64, 128)
+_REFERENCE_HEAD_DIMS = {16, 32, 64, 128, 256}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return N.DTYPE_BF16
+    if t.dtype == torch.float16:
+        return N.DTYPE_F16
+    raise TypeError(f"sps_amd attention supports bfloat16 and float16 inputs, got {t.dtype}")
+
+
+def _kernel_view(t: torch.Tensor) -> torch.Tensor:
+    """Returns t if the kernels can read it in place (unit d stride, 16-byte aligned rows)."""
+    ok = (
+        t.stride(3) == 1
+        and t.data_ptr() % 16 == 0
+        and all(s % 8 == 0 for s in (t.stride(0), t.stride(1), t.stride(2)))
+    )
+    return t if ok else t.contiguous()
+
+
+def _strides(t: torch.Tensor):
+    return N.i64_array((t.stride(0), t.stride(1), t.stride(2)))
+
+
+def _docs_args(docs: Optional[torch.Tensor]):
+    if docs is None:
+        return None, 0, 0
+    if docs.dtype == torch.int64:
+        code = N.DTYPE_I64
+    elif docs.dtype == torch.int32:
+        code = N.DTYPE_I32
+    else:
+        raise TypeError(f"documents_idx_BxT must be int32 or int64, got {docs.dtype}")
+    return docs.data_ptr(), code, docs.stride(0)
+
+
+def _alloc_like_bnhd(q: torch.Tensor) -> torch.Tensor:
+    b, h, n, d = q.shape
+    return torch.empty((b, n, h, d), dtype=q.dtype, device=q.device).transpose(1, 2)
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _workspace(family: int, b: int, h: int, n: int, has_docs: bool, backward: bool, device) -> torch.Tensor:
+    nbytes = N.lib().sps_attn_workspace_bytes(family, b, h, n, int(has_docs), int(backward))
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _validate(q, k, v, family, documents_idx_BxT):
+    head_dim_q, head_dim_k = q.shape[-1], k.shape[-1]
+    head_dim_v = v.shape[-1]
+    assert head_dim_q == head_dim_k and head_dim_k == head_dim_v
+    assert head_dim_k in _REFERENCE_HEAD_DIMS
+    if family != N.FAMILY_FULL:
+        assert q.shape[2] % 2 == 0, "Expected doubled sequence length (2T)."
+    if documents_idx_BxT is not None:
+        assert documents_idx_BxT.shape[0] == q.shape[0]
+        assert documents_idx_BxT.shape[1] == q.shape[2]
+        assert documents_idx_BxT.is_cuda and documents_idx_BxT.is_contiguous()
+    if head_dim_k not in _SUPPORTED_HEAD_DIMS:
+        raise NotImplementedError(f"sps_amd: head_dim {head_dim_k} is not built (supported: {_SUPPORTED_HEAD_DIMS})")
+    if not q.is_cuda:
+        raise RuntimeError("sps_amd attention runs on the GPU only (got a CPU tensor)")
+    if not (k.shape == q.shape and v.shape == q.shape):
+        raise ValueError(f"q, k, v must share one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k and v must share one dtype")
+
+
+def attention_forward(q, k, v, sm_scale, family, window=0, documents_idx_BxT=None, persistent_key_window=None):
+    """Runs the forward kernel; returns (o, lse, q, k, v) with q/k/v as the kernels read them."""
+    q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
+    b, h, n, d = q.shape
+    o = _alloc_like_bnhd(q)
+    lse = torch.empty((b, h, n), dtype=torch.float32, device=q.device)
+    docs_ptr, docs_code, docs_sb = _docs_args(documents_idx_BxT)
+    ws = _workspace(family, b, h, n, documents_idx_BxT is not None, False, q.device)
+    has_pkw = persistent_key_window is not None
+    status = N.lib().sps_attn_fwd(
+        family, b, h, n, d, _dtype_code(q),
+        q.data_ptr(), _strides(q), k.data_ptr(), _strides(k), v.data_ptr(), _strides(v),
+        o.data_ptr(), _strides(o), lse.data_ptr(),
+        docs_ptr, docs_code, docs_sb,
+        float(sm_scale), int(window), int(has_pkw), int(persistent_key_window) if has_pkw else -1,
+        ws.data_ptr(), ws.numel(), _stream(q),
+    )
+    N.check("sps_attn_fwd", status)
+    return o, lse, q, k, v
+
+
+def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, documents_idx_BxT=None,
+                       persistent_key_window=None):
+    """Runs the backward kernels; returns (dq, dk, dv) laid out like q, k, v."""
+    do = _kernel_view(do)
+    b, h, n, d = q.shape
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    docs_ptr, docs_code, docs_sb = _docs_args(documents_idx_BxT)
+    ws = _workspace(family, b, h, n, documents_idx_BxT is not None, True, q.device)
+    has_pkw = persistent_key_window is not None
+    status = N.lib().sps_attn_bwd(
+        family, b, h, n, d, _dtype_code(q),
+        q.data_ptr(), _strides(q), k.data_ptr(), _strides(k), v.data_ptr(), _strides(v),
+        o.data_ptr(), _strides(o), do.data_ptr(), _strides(do), lse.data_ptr(),
+        dq.data_ptr(), _strides(dq), dk.data_ptr(), _strides(dk), dv.data_ptr(), _strides(dv),
+        docs_ptr, docs_code, docs_sb,
+        float(sm_scale), int(window), int(has_pkw), int(persistent_key_window) if has_pkw else -1,
+        ws.data_ptr(), ws.numel(), _stream(q),
+    )
+    N.check("sps_attn_bwd", status)
+    return dq, dk, dv
+
+
+class _Attention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, sm_scale, family, window, documents_idx_BxT, persistent_key_window):
+        _validate(q, k, v, family, documents_idx_BxT)
+        o, lse, qk, kk, vk = attention_forward(
+            q, k, v, sm_scale, family, window, documents_idx_BxT, persistent_key_window
+        )
+        if documents_idx_BxT is not None:
+            ctx.save_for_backward(qk, kk, vk, o, lse, documents_idx_BxT)
+        else:
+            ctx.save_for_backward(qk, kk, vk, o, lse)
+        ctx.sm_scale = float(sm_scale)
+        ctx.family = family
+        ctx.window = int(window)
+        ctx.pkw = persistent_key_window
+        ctx.has_docs = documents_idx_BxT is not None
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        if ctx.has_docs:
+            q, k, v, o, lse, docs = ctx.saved_tensors
+        else:
+            q, k, v, o, lse = ctx.saved_tensors
+            docs = None
+        dq, dk, dv = attention_backward(
+            do, q, k, v, o, lse, ctx.sm_scale, ctx.family, ctx.window, docs, ctx.pkw
+        )
+        return dq, dk, dv, None, None, None, None, None
+
+
+def sps_sliding_attention(
+    q,
+    k,
+    v,
+    sm_scale,
+    temporary_key_window,
+    warp_specialize=True,
+    documents_idx_BxT=None,
+    persistent_key_window=None,
+):
+    """Attention over the interleaved input/<predict> (2T) sequence, SPS variant.
+
+    The persistent (window-exempt) key is the EVEN/input position; the <predict> position (odd) is
+    the temporary key, visible only within ``temporary_key_window`` tokens of the query. The
+    persistent key always self-attends and, when ``persistent_key_window`` is given, is otherwise
+    visible only within that many tokens. ``documents_idx_BxT`` ([B, 2T] ids) confines attention to
+    equal ids. q, k, v: [B, H, 2T, D] bf16/f16. Reference: triton_sps_flash_attention.py:725-753.
+    """
+    del warp_specialize
+    return _Attention.apply(
+        q, k, v, sm_scale, N.FAMILY_SPS, temporary_key_window, documents_idx_BxT, persistent_key_window
+    )
+
+
+def reverse_sps_sliding_attention(
+    q,
+    k,
+    v,
+    sm_scale,
+    temporary_key_window,
+    warp_specialize=True,
+    documents_idx_BxT=None,
+    persistent_key_window=None,
+):
+    """As ``sps_sliding_attention`` with the persistent key at the ODD/<predict> position.
+
+    Used by the Reverse-SPS and Delayed-State models. Reference:
+    triton_reverse_sps_flash_attention.py:827-853.
+    """
+    del warp_specialize
+    return _Attention.apply(
+        q, k, v, sm_scale, N.FAMILY_REVERSE_SPS, temporary_key_window, documents_idx_BxT,
+        persistent_key_window,
+    )
+
+
+def full_attention(
+    q,
+    k,
+    v,
+    sm_scale,
+    warp_specialize=True,
+    documents_idx_BxT=None,
+):
+    """Document-masked causal attention (Standard model). q, k, v: [B, H, T, D].
+
+    A query attends causally to keys with its document id (or to all causal keys when
+    ``documents_idx_BxT`` is None). Reference: triton_full_flash_attention.py:679-709.
+    """
+    del warp_specialize
+    return _Attention.apply(q, k, v, sm_scale, N.FAMILY_FULL, 0, documents_idx_BxT, None)
+
+
+def attention_mask(family: int, n: int, documents_idx_BxT: Optional[torch.Tensor] = None, *, batch: int = 1,
+                   window: int = 0, persistent_key_window: Optional[int] = None, schedule: int = 0,
+                   device=None) -> torch.Tensor:
+    """Materialises the [B, N, N] uint8 mask the kernels evaluate (schedule 0: forward/dQ block
+    schedule, 1: dK/dV block schedule). A verification entry point; see include/sps_attn.h."""
+    if documents_idx_BxT is not None:
+        batch = documents_idx_BxT.shape[0]
+        device = documents_idx_BxT.device
+    device = torch.device(device if device is not None else "cuda")
+    mask = torch.zeros((batch, n, n), dtype=torch.uint8, device=device)
+    docs_ptr, docs_code, docs_sb = _docs_args(documents_idx_BxT)
+    ws = _workspace(family, batch, 1, n, documents_idx_BxT is not None, False, device)
+    has_pkw = persistent_key_window is not None
+    status = N.lib().sps_attn_mask(
+        family, batch, n, docs_ptr, docs_code, docs_sb, int(window), int(has_pkw),
+        int(persistent_key_window) if has_pkw else -1, int(schedule), mask.data_ptr(),
+        ws.data_ptr(), ws.numel(), torch.cuda.current_stream(device).cuda_stream,
+    )
+    N.check("sps_attn_mask", status)
+    return mask
+
+
+def default_sm_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,350 @@
+// C ABI of libsps_attn.so: argument validation, workspace layout and kernel dispatch.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/sps_attn.h"
+#include "attn_kernels.hpp"
+#include "decode_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return SPS_OK;
+  return fail(SPS_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_tensor(const char* name, const void* p, const int64_t* st, int need) {
+  if (!need) return SPS_OK;
+  if (!p) return fail(SPS_E_INVALID, "%s: null pointer", name);
+  if (!st) return fail(SPS_E_INVALID, "%s: null strides", name);
+  if (!aligned16(p)) return fail(SPS_E_INVALID, "%s: base pointer must be 16-byte aligned", name);
+  for (int i = 0; i < 3; ++i)
+    if (st[i] % 8 != 0)
+      return fail(SPS_E_INVALID, "%s: stride %d (%lld) must be a multiple of 8 elements", name, i,
+                  (long long)st[i]);
+  return SPS_OK;
+}
+
+sps::Strides3 strides(const int64_t* st) {
+  sps::Strides3 s = {0, 0, 0};
+  if (st) s = {st[0], st[1], st[2]};
+  return s;
+}
+
+bool supported_head_dim(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+
+struct AttnLayout {
+  size_t gmin, gmax, delta, total;
+};
+
+AttnLayout attn_layout(int family, int B, int H, int N, int has_docs, int backward) {
+  (void)family;
+  AttnLayout l = {0, 0, 0, 0};
+  const size_t NG = (size_t)(N + sps::kGranule - 1) / sps::kGranule;
+  size_t off = 0;
+  if (has_docs) {
+    l.gmin = off;
+    off = align_up(off + (size_t)B * NG * sizeof(int64_t));
+    l.gmax = off;
+    off = align_up(off + (size_t)B * NG * sizeof(int64_t));
+  }
+  if (backward) {
+    l.delta = off;
+    off = align_up(off + (size_t)B * H * N * sizeof(float));
+  }
+  l.total = off;
+  return l;
+}
+
+// Fills the mask-related fields of the argument block and validates the common scalars.
+int setup_common(sps::AttnArgs& a, int family, int B, int H, int N, const void* docs, int docs_dtype,
+                 int64_t docs_stride_b, int window, int has_pkw, int pkw, void* workspace,
+                 size_t workspace_bytes, int backward) {
+  if (family < SPS_FAMILY_FULL || family > SPS_FAMILY_REVERSE_SPS)
+    return fail(SPS_E_INVALID, "unknown attention family %d", family);
+  if (B < 0 || H < 0 || N < 0) return fail(SPS_E_INVALID, "negative size B=%d H=%d N=%d", B, H, N);
+  if (family != SPS_FAMILY_FULL && (N % 2) != 0)
+    return fail(SPS_E_INVALID, "SPS families need an even sequence length (2T), got N=%d", N);
+  if (docs && docs_dtype != SPS_DTYPE_I32 && docs_dtype != SPS_DTYPE_I64)
+    return fail(SPS_E_INVALID, "document ids must be int32 or int64 (dtype code %d)", docs_dtype);
+  const AttnLayout l = attn_layout(family, B, H, N, docs != nullptr, backward);
+  if (workspace_bytes < l.total)
+    return fail(SPS_E_WORKSPACE, "workspace too small: %zu bytes < %zu", workspace_bytes, l.total);
+  if (l.total > 0 && !workspace) return fail(SPS_E_INVALID, "workspace: null pointer");
+  char* ws = static_cast<char*>(workspace);
+  std::memset(&a, 0, sizeof(a));
+  a.docs = docs;
+  a.docs_i64 = docs_dtype == SPS_DTYPE_I64;
+  a.docs_sb = docs_stride_b;
+  a.NG = (N + sps::kGranule - 1) / sps::kGranule;
+  a.gmin = docs ? reinterpret_cast<int64_t*>(ws + l.gmin) : nullptr;
+  a.gmax = docs ? reinterpret_cast<int64_t*>(ws + l.gmax) : nullptr;
+  a.delta = backward ? reinterpret_cast<float*>(ws + l.delta) : nullptr;
+  a.B = B;
+  a.H = H;
+  a.m.family = family;
+  a.m.P = family == SPS_FAMILY_REVERSE_SPS ? 1 : 0;
+  a.m.N = N;
+  a.m.window = window;
+  a.m.has_pkw = has_pkw ? 1 : 0;
+  a.m.pkw = pkw;
+  a.m.has_docs = docs != nullptr;
+  return SPS_OK;
+}
+
+int check_scale(float sm_scale) {
+  if (!(sm_scale > 0.f) || !std::isfinite(sm_scale))
+    return fail(SPS_E_UNSUPPORTED, "sm_scale must be finite and > 0 (got %g)", (double)sm_scale);
+  return SPS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sps_version(void) { return "sps_attn 0.1.0 (gfx950)"; }
+
+int sps_last_error(char* buf, size_t len) {
+  if (buf && len > 0) {
+    std::strncpy(buf, g_last_error.c_str(), len - 1);
+    buf[len - 1] = '\0';
+  }
+  return (int)g_last_error.size();
+}
+
+size_t sps_attn_workspace_bytes(int family, int B, int H, int N, int has_docs, int backward) {
+  if (B < 0 || H < 0 || N < 0) return 0;
+  return attn_layout(family, B, H, N, has_docs, backward).total;
+}
+
+int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype, const void* q, const int64_t* q_strides,
+                 const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides, void* o,
+                 const int64_t* o_strides, float* lse, const void* docs, int docs_dtype,
+                 int64_t docs_stride_b, float sm_scale, int window, int has_pkw, int pkw, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  sps::AttnArgs a;
+  int rc = setup_common(a, family, B, H, N, docs, docs_dtype, docs_stride_b, window, has_pkw, pkw,
+                        workspace, workspace_bytes, 0);
+  if (rc) return rc;
+  if (!supported_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "head_dim %d not supported", D);
+  if (dtype != SPS_DTYPE_BF16 && dtype != SPS_DTYPE_F16)
+    return fail(SPS_E_UNSUPPORTED, "attention dtype code %d not supported (bf16, f16)", dtype);
+  if ((rc = check_scale(sm_scale))) return rc;
+  const int need = (int64_t)B * H * N > 0;
+  if ((rc = check_tensor("q", q, q_strides, need)) || (rc = check_tensor("k", k, k_strides, need)) ||
+      (rc = check_tensor("v", v, v_strides, need)) || (rc = check_tensor("o", o, o_strides, need)))
+    return rc;
+  if (need && !lse) return fail(SPS_E_INVALID, "lse: null pointer");
+  if (!need) return SPS_OK;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.out = static_cast<uint16_t*>(o);
+  a.sq = strides(q_strides);
+  a.sk = strides(k_strides);
+  a.sv = strides(v_strides);
+  a.sout = strides(o_strides);
+  a.lse = lse;
+  a.sm_scale = sm_scale;
+  a.scale2 = sm_scale * 1.4426950408889634f;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (docs && (rc = hip_status(sps::launch_doc_granules(a, s), "document prepass"))) return rc;
+  return hip_status(sps::launch_attn_fwd(a, D, dtype == SPS_DTYPE_F16, s), "attention forward");
+}
+
+int sps_attn_bwd(int family, int B, int H, int N, int D, int dtype, const void* q, const int64_t* q_strides,
+                 const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                 const void* o, const int64_t* o_strides, const void* dout, const int64_t* dout_strides,
+                 const float* lse, void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides,
+                 void* dv, const int64_t* dv_strides, const void* docs, int docs_dtype, int64_t docs_stride_b,
+                 float sm_scale, int window, int has_pkw, int pkw, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  g_last_error.clear();
+  sps::AttnArgs a;
+  int rc = setup_common(a, family, B, H, N, docs, docs_dtype, docs_stride_b, window, has_pkw, pkw,
+                        workspace, workspace_bytes, 1);
+  if (rc) return rc;
+  if (!supported_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "head_dim %d not supported", D);
+  if (dtype != SPS_DTYPE_BF16 && dtype != SPS_DTYPE_F16)
+    return fail(SPS_E_UNSUPPORTED, "attention dtype code %d not supported (bf16, f16)", dtype);
+  if ((rc = check_scale(sm_scale))) return rc;
+  const int need = (int64_t)B * H * N > 0;
+  if ((rc = check_tensor("q", q, q_strides, need)) || (rc = check_tensor("k", k, k_strides, need)) ||
+      (rc = check_tensor("v", v, v_strides, need)) || (rc = check_tensor("o", o, o_strides, need)) ||
+      (rc = check_tensor("dout", dout, dout_strides, need)) || (rc = check_tensor("dq", dq, dq_strides, need)) ||
+      (rc = check_tensor("dk", dk, dk_strides, need)) || (rc = check_tensor("dv", dv, dv_strides, need)))
+    return rc;
+  if (need && !lse) return fail(SPS_E_INVALID, "lse: null pointer");
+  if (!need) return SPS_OK;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.o = static_cast<const uint16_t*>(o);
+  a.dO = static_cast<const uint16_t*>(dout);
+  a.dq = static_cast<uint16_t*>(dq);
+  a.dk = static_cast<uint16_t*>(dk);
+  a.dv = static_cast<uint16_t*>(dv);
+  a.sq = strides(q_strides);
+  a.sk = strides(k_strides);
+  a.sv = strides(v_strides);
+  a.so = strides(o_strides);
+  a.sdo = strides(dout_strides);
+  a.sdq = strides(dq_strides);
+  a.sdk = strides(dk_strides);
+  a.sdv = strides(dv_strides);
+  a.lse = const_cast<float*>(lse);
+  a.sm_scale = sm_scale;
+  a.scale2 = sm_scale * 1.4426950408889634f;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (docs && (rc = hip_status(sps::launch_doc_granules(a, s), "document prepass"))) return rc;
+  return hip_status(sps::launch_attn_bwd(a, D, dtype == SPS_DTYPE_F16, s), "attention backward");
+}
+
+int sps_attn_mask(int family, int B, int N, const void* docs, int docs_dtype, int64_t docs_stride_b, int window,
+                  int has_pkw, int pkw, int schedule, uint8_t* mask, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  g_last_error.clear();
+  sps::AttnArgs a;
+  int rc = setup_common(a, family, B, 1, N, docs, docs_dtype, docs_stride_b, window, has_pkw, pkw, workspace,
+                        workspace_bytes, 0);
+  if (rc) return rc;
+  if (schedule != 0 && schedule != 1) return fail(SPS_E_INVALID, "schedule must be 0 or 1");
+  if ((int64_t)B * N == 0) return SPS_OK;
+  if (!mask) return fail(SPS_E_INVALID, "mask: null pointer");
+  a.mask_out = mask;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (docs && (rc = hip_status(sps::launch_doc_granules(a, s), "document prepass"))) return rc;
+  return hip_status(sps::launch_mask_dump(a, schedule, s), "mask dump");
+}
+
+static int kv_bytes(int kv_dtype) { return kv_dtype == SPS_DTYPE_F32 ? 4 : 2; }
+
+static bool decode_head_dim(int D) { return D == 16 || D == 32 || D == 64 || D == 128 || D == 256; }
+
+size_t sps_decode_workspace_bytes(int B, int H, int D, int nq, int kv_dtype, int n_seg, const int64_t* seg_scan) {
+  if (!decode_head_dim(D) || B < 0 || H < 0 || n_seg < 0 || n_seg > sps::kMaxDecodeSegs) return 0;
+  const int ck = sps::decode_chunk_keys(D, kv_bytes(kv_dtype));
+  int64_t chunks = 0;
+  for (int s = 0; s < n_seg; ++s) chunks += (seg_scan[s] + ck - 1) / ck;
+  const size_t bytes = (size_t)B * H * chunks * nq * sps::decode_record_floats(D) * sizeof(float);
+  return align_up(bytes);
+}
+
+int sps_decode(int B, int H, int D, int nq, const float* q, const int64_t* q_strides, int kv_dtype, int n_seg,
+               const void* const* seg_k, const int64_t* seg_k_strides, const void* const* seg_v,
+               const int64_t* seg_v_strides, const void* const* seg_len, const int* seg_len_dtype,
+               const int* seg_len_per_head, const int64_t* seg_scan, int n_extra, const float* const* extra_k,
+               const float* const* extra_v, const int64_t* extra_strides, const int* extra_query_mask,
+               float sm_scale, float* out, const int64_t* out_strides, void* workspace, size_t workspace_bytes,
+               void* stream) {
+  g_last_error.clear();
+  if (B < 0 || H < 0) return fail(SPS_E_INVALID, "negative size B=%d H=%d", B, H);
+  if (nq != 1 && nq != 2) return fail(SPS_E_INVALID, "nq must be 1 or 2 (got %d)", nq);
+  if (!decode_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "decode head_dim %d not supported", D);
+  if (kv_dtype != SPS_DTYPE_BF16 && kv_dtype != SPS_DTYPE_F16 && kv_dtype != SPS_DTYPE_F32)
+    return fail(SPS_E_UNSUPPORTED, "K/V dtype code %d not supported", kv_dtype);
+  if (n_seg < 0 || n_seg > sps::kMaxDecodeSegs)
+    return fail(SPS_E_INVALID, "at most %d segments (got %d)", sps::kMaxDecodeSegs, n_seg);
+  if (n_extra < 0 || n_extra > sps::kMaxDecodeExtras)
+    return fail(SPS_E_INVALID, "at most %d extra keys (got %d)", sps::kMaxDecodeExtras, n_extra);
+  if ((int64_t)B * H == 0) return SPS_OK;
+  if (!q || !q_strides || !out || !out_strides) return fail(SPS_E_INVALID, "q/out: null pointer");
+  if (!(std::isfinite(sm_scale))) return fail(SPS_E_INVALID, "sm_scale must be finite");
+  const size_t need = sps_decode_workspace_bytes(B, H, D, nq, kv_dtype, n_seg, seg_scan);
+  if (workspace_bytes < need) return fail(SPS_E_WORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, need);
+  sps::DecodeArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.B = B;
+  a.H = H;
+  a.NQ = nq;
+  a.n_seg = n_seg;
+  a.n_extra = n_extra;
+  const int kb = kv_bytes(kv_dtype);
+  const int epl = 16 / kb;
+  const int ck = sps::decode_chunk_keys(D, kb);
+  int chunk = 0;
+  for (int s = 0; s < n_seg; ++s) {
+    sps::DecodeSeg& sg = a.seg[s];
+    if (seg_scan[s] < 0 || seg_scan[s] > INT32_MAX)
+      return fail(SPS_E_INVALID, "segment %d: scan length %lld out of range", s, (long long)seg_scan[s]);
+    sg.scan = (int)seg_scan[s];
+    sg.chunk_base = chunk;
+    chunk += (sg.scan + ck - 1) / ck;
+    if (sg.scan == 0) continue;
+    if (!seg_k[s] || !seg_v[s] || !seg_len[s]) return fail(SPS_E_INVALID, "segment %d: null pointer", s);
+    if (!aligned16(seg_k[s]) || !aligned16(seg_v[s]))
+      return fail(SPS_E_INVALID, "segment %d: K/V base must be 16-byte aligned", s);
+    const int64_t* ks = seg_k_strides + 3 * s;
+    const int64_t* vs = seg_v_strides + 3 * s;
+    for (int i = 0; i < 3; ++i)
+      if (ks[i] % epl != 0 || vs[i] % epl != 0)
+        return fail(SPS_E_INVALID, "segment %d: strides must be multiples of 16 bytes", s);
+    if (seg_len_dtype[s] != SPS_DTYPE_I32 && seg_len_dtype[s] != SPS_DTYPE_I64)
+      return fail(SPS_E_INVALID, "segment %d: lengths must be int32 or int64", s);
+    sg.k = seg_k[s];
+    sg.v = seg_v[s];
+    sg.ksb = ks[0];
+    sg.ksh = ks[1];
+    sg.kst = ks[2];
+    sg.vsb = vs[0];
+    sg.vsh = vs[1];
+    sg.vst = vs[2];
+    sg.len = seg_len[s];
+    sg.len_i64 = seg_len_dtype[s] == SPS_DTYPE_I64;
+    sg.len_per_head = seg_len_per_head[s] != 0;
+  }
+  // Segments with scan 0 own no chunk; give them a valid (never read) length pointer source.
+  for (int s = 0; s < n_seg; ++s) {
+    if (a.seg[s].scan == 0) {
+      a.seg[s].len = nullptr;
+    }
+  }
+  a.n_chunks = chunk;
+  a.chunk_keys = ck;
+  for (int e = 0; e < n_extra; ++e) {
+    if (!extra_k[e] || !extra_v[e]) return fail(SPS_E_INVALID, "extra %d: null pointer", e);
+    a.ek[e] = extra_k[e];
+    a.ev[e] = extra_v[e];
+    a.emask[e] = extra_query_mask[e];
+  }
+  if (n_extra > 0) {
+    a.e_sb = extra_strides[0];
+    a.e_sh = extra_strides[1];
+  }
+  a.q = q;
+  a.q_sb = q_strides[0];
+  a.q_ss = q_strides[1];
+  a.q_sh = q_strides[2];
+  a.out = out;
+  a.o_sb = out_strides[0];
+  a.o_ss = out_strides[1];
+  a.o_sh = out_strides[2];
+  a.scale2 = sm_scale * 1.4426950408889634f;
+  a.part = static_cast<float*>(workspace);
+  return hip_status(sps::launch_decode(a, D, kv_dtype, static_cast<hipStream_t>(stream)), "decode");
+}
+
+}  // extern "C"

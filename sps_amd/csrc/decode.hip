@@ -1,0 +1,331 @@
+// Segmented decode attention (1 or 2 queries per (batch, head)) over up to 3 variable-length KV
+// segments plus up to 2 single-token "extra" keys, gfx950.
+//
+// Reference semantics: _segmented_q1_attention_kernel / _segmented_q2_attention_kernel
+// (utils/decode_attention.py:79-188, 267-368): fp32 scores from 16-bit K/V, online softmax,
+// key t of a segment is valid iff t < min(max(len, 0), scan_len), output 0 when no key is valid.
+// Extras are always valid; in the q=2 form the first extra (current input key) is seen by both
+// queries and the second (current <predict> key) by query 1 only.
+//
+// The pass is HBM-bound (one query row per 256 B of K+V at D = 64), so it is organised for
+// bandwidth, not MFMA: every segment is cut into fixed chunks of keys, one workgroup per
+// (chunk, head, batch). Each wave streams its slice of the chunk with 16-byte coalesced loads
+// (all loads issued before any arithmetic), computes fp32 dot products with a short lane
+// reduction, and keeps an exp2-domain partial softmax; the four waves merge in LDS and the
+// workgroup writes one (acc[D], m, l) partial. Only live keys are read: chunks past the live
+// length exit before touching K/V. A second small kernel merges the partials with the extras.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "cdna4.hpp"
+#include "decode_kernels.hpp"
+
+namespace sps {
+
+struct KvBF16 {
+  using raw = uint16_t;
+  static __device__ __forceinline__ float cvt(uint16_t x) { return ElemBF16::to_f32(x); }
+};
+struct KvF16 {
+  using raw = uint16_t;
+  static __device__ __forceinline__ float cvt(uint16_t x) { return ElemF16::to_f32(x); }
+};
+struct KvF32 {
+  using raw = float;
+  static __device__ __forceinline__ float cvt(float x) { return x; }
+};
+
+template <class KV>
+__device__ __forceinline__ void unpack16(const u32x4_t w, float* out) {
+  if constexpr (sizeof(typename KV::raw) == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = KV::cvt((uint16_t)(w[i] & 0xffffu));
+      out[2 * i + 1] = KV::cvt((uint16_t)(w[i] >> 16));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __builtin_bit_cast(float, w[i]);
+  }
+}
+
+__device__ __forceinline__ int seg_live_len(const DecodeSeg& sg, int b, int h, int H) {
+  if (sg.scan == 0) return 0;
+  const int64_t idx = sg.len_per_head ? (int64_t)b * H + h : b;
+  int64_t len = sg.len_i64 ? reinterpret_cast<const int64_t*>(sg.len)[idx]
+                           : (int64_t) reinterpret_cast<const int32_t*>(sg.len)[idx];
+  if (len < 0) len = 0;
+  if (len > sg.scan) len = sg.scan;
+  return (int)len;
+}
+
+template <int W>
+__device__ __forceinline__ float xor_sum(float x) {
+#pragma unroll
+  for (int o = 1; o < W; o <<= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// Reduction over lanes that differ only in bits [log2(LPR), 6): the row groups of a wave.
+template <int LPR>
+__device__ __forceinline__ float group_max(float x) {
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+template <int LPR>
+__device__ __forceinline__ float group_sum(float x) {
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+template <int D, int NQ, class KV>
+__global__ __launch_bounds__(256) void decode_partial_kernel(const DecodeArgs a) {
+  constexpr int EPL = 16 / (int)sizeof(typename KV::raw);  // elements per 16-byte load
+  constexpr int LPR = D / EPL;                              // lanes per key row
+  constexpr int RPP = 64 / LPR;                             // rows per wave pass
+  constexpr int PASS = DecodeGeom<D, sizeof(typename KV::raw)>::PASS;
+  constexpr int KW = RPP * PASS;                            // keys per wave
+  constexpr int CK = 4 * KW;                                // keys per workgroup chunk
+  static_assert(CK == DecodeGeom<D, sizeof(typename KV::raw)>::CHUNK, "chunk geometry");
+  __shared__ float s_m[4][NQ], s_l[4][NQ];
+  __shared__ __attribute__((aligned(16))) float s_acc[4][NQ][D];
+
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  int si = 0;
+  while (si + 1 < a.n_seg && c >= a.seg[si + 1].chunk_base) ++si;
+  const DecodeSeg sg = a.seg[si];
+  const int live = seg_live_len(sg, b, h, a.H);
+  const int t0 = (c - sg.chunk_base) * CK;
+  if (t0 >= live) return;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane / LPR, cc = lane % LPR;
+
+  // This lane's query slice(s): elements cc*EPL .. +EPL.
+  float qv[NQ][EPL];
+#pragma unroll
+  for (int qi = 0; qi < NQ; ++qi) {
+    const float* qrow = a.q + b * a.q_sb + qi * a.q_ss + h * a.q_sh + cc * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) qv[qi][e] = qrow[e];
+  }
+
+  using raw_t = typename KV::raw;
+  const raw_t* kb = reinterpret_cast<const raw_t*>(sg.k) + b * sg.ksb + h * sg.ksh + cc * EPL;
+  const raw_t* vb = reinterpret_cast<const raw_t*>(sg.v) + b * sg.vsb + h * sg.vsh + cc * EPL;
+  const int tw = t0 + wave * KW + r;
+  u32x4_t kr[PASS], vr[PASS];
+#pragma unroll
+  for (int j = 0; j < PASS; ++j) {
+    const int t = tw + j * RPP;
+    u32x4_t z = {0u, 0u, 0u, 0u};
+    kr[j] = t < live ? *reinterpret_cast<const u32x4_t*>(kb + (int64_t)t * sg.kst) : z;
+  }
+#pragma unroll
+  for (int j = 0; j < PASS; ++j) {
+    const int t = tw + j * RPP;
+    u32x4_t z = {0u, 0u, 0u, 0u};
+    vr[j] = t < live ? *reinterpret_cast<const u32x4_t*>(vb + (int64_t)t * sg.vst) : z;
+  }
+
+  float sc[NQ][PASS];
+#pragma unroll
+  for (int j = 0; j < PASS; ++j) {
+    float kf[EPL];
+    unpack16<KV>(kr[j], kf);
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) d = fmaf(qv[qi][e], kf[e], d);
+      d = xor_sum<LPR>(d);
+      sc[qi][j] = (tw + j * RPP < live) ? d * a.scale2 : -INFINITY;
+    }
+  }
+
+  float acc[NQ][EPL];
+  float mw[NQ], lw[NQ];
+#pragma unroll
+  for (int qi = 0; qi < NQ; ++qi) {
+    float mx = sc[qi][0];
+#pragma unroll
+    for (int j = 1; j < PASS; ++j) mx = fmaxf(mx, sc[qi][j]);
+    mx = group_max<LPR>(mx);
+    const float mu = mx == -INFINITY ? 0.f : mx;
+    float l = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[qi][e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < PASS; ++j) {
+      const float p = fast_exp2(sc[qi][j] - mu);
+      l += p;
+      float vf[EPL];
+      unpack16<KV>(vr[j], vf);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[qi][e] = fmaf(p, vf[e], acc[qi][e]);
+    }
+    mw[qi] = mx;
+    lw[qi] = group_sum<LPR>(l);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[qi][e] = group_sum<LPR>(acc[qi][e]);
+  }
+
+  if (r == 0) {
+#pragma unroll
+    for (int qi = 0; qi < NQ; ++qi) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) s_acc[wave][qi][cc * EPL + e] = acc[qi][e];
+      if (cc == 0) {
+        s_m[wave][qi] = mw[qi];
+        s_l[wave][qi] = lw[qi];
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int REC = DecodeGeom<D, 2>::REC;
+  float* out = a.part + (((int64_t)(b * a.H + h) * a.n_chunks + c) * NQ) * REC;
+  for (int i = tid; i < NQ * D; i += 256) {
+    const int qi = i / D, d = i - qi * D;
+    float M = s_m[0][qi];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w][qi]);
+    const float mu = M == -INFINITY ? 0.f : M;
+    float A = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = fast_exp2(s_m[w][qi] - mu);
+      A = fmaf(f, s_acc[w][qi][d], A);
+      L = fmaf(f, s_l[w][qi], L);
+    }
+    out[qi * REC + d] = A;
+    if (d == 0) {
+      out[qi * REC + D] = M;
+      out[qi * REC + D + 1] = L;
+    }
+  }
+}
+
+// One wave per (head, batch): merges the chunk partials and the extra keys, normalises, writes fp32.
+template <int D, int NQ>
+__global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
+  constexpr int DPL = (D + 63) / 64;  // output elements per lane
+  constexpr int REC = DecodeGeom<D, 2>::REC;
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  int live[3];
+  for (int s = 0; s < a.n_seg; ++s) live[s] = seg_live_len(a.seg[s], b, h, a.H);
+  const float* part = a.part + ((int64_t)(b * a.H + h) * a.n_chunks) * NQ * REC;
+
+  for (int qi = 0; qi < NQ; ++qi) {
+    const float* qrow = a.q + b * a.q_sb + qi * a.q_ss + h * a.q_sh;
+    float es[2];
+    bool eon[2];
+    for (int e = 0; e < a.n_extra; ++e) {
+      eon[e] = (a.emask[e] >> qi) & 1;
+      float d = 0.f;
+      const float* kr = a.ek[e] + b * a.e_sb + h * a.e_sh;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) {
+        const int dd = lane + 64 * i;
+        if (dd < D) d = fmaf(qrow[dd], kr[dd], d);
+      }
+      d = xor_sum<64>(d);
+      es[e] = d * a.scale2;
+    }
+    float M = -INFINITY;
+    for (int s = 0; s < a.n_seg; ++s) {
+      const int nc = (live[s] + a.chunk_keys - 1) / a.chunk_keys;
+      for (int c = a.seg[s].chunk_base; c < a.seg[s].chunk_base + nc; ++c)
+        M = fmaxf(M, part[(c * NQ + qi) * REC + D]);
+    }
+    for (int e = 0; e < a.n_extra; ++e)
+      if (eon[e]) M = fmaxf(M, es[e]);
+    const float mu = M == -INFINITY ? 0.f : M;
+    float L = 0.f, A[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) A[i] = 0.f;
+    for (int s = 0; s < a.n_seg; ++s) {
+      const int nc = (live[s] + a.chunk_keys - 1) / a.chunk_keys;
+      for (int c = a.seg[s].chunk_base; c < a.seg[s].chunk_base + nc; ++c) {
+        const float* rec = part + (c * NQ + qi) * REC;
+        const float f = fast_exp2(rec[D] - mu);
+        L = fmaf(f, rec[D + 1], L);
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) {
+          const int dd = lane + 64 * i;
+          if (dd < D) A[i] = fmaf(f, rec[dd], A[i]);
+        }
+      }
+    }
+    for (int e = 0; e < a.n_extra; ++e) {
+      if (!eon[e]) continue;
+      const float f = fast_exp2(es[e] - mu);
+      L += f;
+      const float* vr = a.ev[e] + b * a.e_sb + h * a.e_sh;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) {
+        const int dd = lane + 64 * i;
+        if (dd < D) A[i] = fmaf(f, vr[dd], A[i]);
+      }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    float* orow = a.out + b * a.o_sb + qi * a.o_ss + h * a.o_sh;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+      const int dd = lane + 64 * i;
+      if (dd < D) orow[dd] = A[i] * inv;
+    }
+  }
+}
+
+template <int D, int NQ, class KV>
+static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
+  if (a.B == 0 || a.H == 0) return hipSuccess;
+  if (a.n_chunks > 0) {
+    hipLaunchKernelGGL((decode_partial_kernel<D, NQ, KV>), dim3(a.n_chunks, a.H, a.B), dim3(256), 0,
+                       stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((decode_merge_kernel<D, NQ>), dim3(a.H, a.B), dim3(64), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <int D, int NQ>
+static hipError_t launch_decode_kv(const DecodeArgs& a, int kv_dtype, hipStream_t stream) {
+  switch (kv_dtype) {
+    case 0:
+      return launch_decode_t<D, NQ, KvBF16>(a, stream);
+    case 1:
+      return launch_decode_t<D, NQ, KvF16>(a, stream);
+    case 2:
+      return launch_decode_t<D, NQ, KvF32>(a, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+template <int D>
+static hipError_t launch_decode_d(const DecodeArgs& a, int kv_dtype, hipStream_t stream) {
+  return a.NQ == 1 ? launch_decode_kv<D, 1>(a, kv_dtype, stream) : launch_decode_kv<D, 2>(a, kv_dtype, stream);
+}
+
+hipError_t launch_decode(const DecodeArgs& a, int D, int kv_dtype, hipStream_t stream) {
+  switch (D) {
+    case 16:
+      return launch_decode_d<16>(a, kv_dtype, stream);
+    case 32:
+      return launch_decode_d<32>(a, kv_dtype, stream);
+    case 64:
+      return launch_decode_d<64>(a, kv_dtype, stream);
+    case 128:
+      return launch_decode_d<128>(a, kv_dtype, stream);
+    case 256:
+      return launch_decode_d<256>(a, kv_dtype, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace sps

@@ -1,0 +1,286 @@
+"""Drop-in segmented decode attention for SPS-family (and Standard-model) generation.
+
+Keeps the reference names, signatures and error conventions of utils/decode_attention.py
+(src/modeling/models/ of lil-lab/sps):
+
+* ``KVSegment``                     <- decode_attention.py:21-32
+* ``triton_segmented_q1_attention`` <- decode_attention.py:393-480 (returns None when unsupported)
+* ``triton_segmented_q2_attention`` <- decode_attention.py:483-594 (raises RuntimeError)
+* ``masked_kv_attention``           <- decode_attention.py:597-704
+
+The names still say "triton" because callers import them by those names; every path here runs the
+HIP kernels of libsps_attn.so. There is no CPU path: ``masked_kv_attention`` on CPU tensors raises.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from . import _native as N
+
+_KV_DTYPES = {torch.bfloat16: N.DTYPE_BF16, torch.float16: N.DTYPE_F16, torch.float32: N.DTYPE_F32}
+_DECODE_HEAD_DIMS = (16, 32, 64, 128, 256)
+
+
+@dataclass
+class KVSegment:
+    """A contiguous block of keys/values with per-element validity lengths.
+
+    k, v: [B, H, max_T, D]; lengths: [B, H] (per head) or [B] (shared across heads);
+    max_len_cap: optional host-side cap on the scanned length.
+    """
+
+    k: Tensor
+    v: Tensor
+    lengths: Tensor
+    max_len_cap: int | None = None
+
+
+def _segment_scan_len(seg: KVSegment) -> int:
+    """Number of leading storage rows a segment may contribute (reference decode_attention.py:381-390)."""
+    max_t = int(seg.k.size(2))
+    if max_t == 0:
+        return 0
+    if seg.max_len_cap is None:
+        return max_t
+    cap = int(seg.max_len_cap)
+    if cap < 0:
+        raise ValueError(f"KVSegment.max_len_cap must be non-negative, got {cap}")
+    return max(1, min(max_t, cap))
+
+
+def _len_dtype(lengths: Tensor) -> int:
+    if lengths.dtype == torch.int64:
+        return N.DTYPE_I64
+    if lengths.dtype == torch.int32:
+        return N.DTYPE_I32
+    raise TypeError(f"segment lengths must be int32 or int64, got {lengths.dtype}")
+
+
+def _run_decode(q_f32: Tensor, nq: int, segments, extras, extra_masks, out: Tensor) -> Tensor:
+    """Calls sps_decode. q_f32: [B, nq, H, D] fp32; extras: list of (k, v) fp32 [B, H, D]."""
+    b, _, h, d = q_f32.shape
+    kv_dtype = N.DTYPE_BF16
+    if segments:
+        kv_dtype = _KV_DTYPES[segments[0].k.dtype]
+    scans = [_segment_scan_len(s) for s in segments]
+    lens = [s.lengths.contiguous() for s in segments]
+    lib = N.lib()
+    scan_arr = N.i64_array(scans)
+    ws_bytes = lib.sps_decode_workspace_bytes(b, h, d, nq, kv_dtype, len(segments), scan_arr)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q_f32.device)
+    k_strides, v_strides = [], []
+    for s in segments:
+        k_strides += [s.k.stride(0), s.k.stride(1), s.k.stride(2)]
+        v_strides += [s.v.stride(0), s.v.stride(1), s.v.stride(2)]
+    ek = [e[0] for e in extras]
+    ev = [e[1] for e in extras]
+    e_strides = (ek[0].stride(0), ek[0].stride(1)) if extras else (0, 0)
+    status = lib.sps_decode(
+        b, h, d, nq,
+        q_f32.data_ptr(), N.i64_array((q_f32.stride(0), q_f32.stride(1), q_f32.stride(2))),
+        kv_dtype, len(segments),
+        N.ptr_array([s.k.data_ptr() for s in segments]), N.i64_array(k_strides),
+        N.ptr_array([s.v.data_ptr() for s in segments]), N.i64_array(v_strides),
+        N.ptr_array([ln.data_ptr() for ln in lens]), N.i32_array([_len_dtype(ln) for ln in lens]),
+        N.i32_array([int(ln.dim() == 2) for ln in lens]), scan_arr,
+        len(extras), N.ptr_array([t.data_ptr() for t in ek]), N.ptr_array([t.data_ptr() for t in ev]),
+        N.i64_array(e_strides), N.i32_array(extra_masks),
+        1.0 / math.sqrt(d), out.data_ptr(), N.i64_array((out.stride(0), out.stride(1), out.stride(2))),
+        ws.data_ptr(), ws.numel(), torch.cuda.current_stream(q_f32.device).cuda_stream,
+    )
+    N.check("sps_decode", status)
+    return out
+
+
+def _segments_compatible(segments, batch_size, n_head, head_dim, device) -> bool:
+    dtypes = {s.k.dtype for s in segments} | {s.v.dtype for s in segments}
+    if len(dtypes) > 1 or (dtypes and next(iter(dtypes)) not in _KV_DTYPES):
+        return False
+    for seg in segments:
+        if seg.k.dim() != 4 or seg.v.dim() != 4 or seg.k.shape != seg.v.shape:
+            return False
+        if seg.k.size(0) != batch_size or seg.k.size(1) != n_head or seg.k.size(3) != head_dim:
+            return False
+        if seg.lengths.device != device or seg.lengths.dim() not in (1, 2):
+            return False
+        if seg.lengths.dtype not in (torch.int32, torch.int64):
+            return False
+        if seg.lengths.dim() == 2 and tuple(seg.lengths.shape) != (batch_size, n_head):
+            return False
+        if seg.lengths.dim() == 1 and seg.lengths.shape[0] != batch_size:
+            return False
+        esize = seg.k.element_size()
+        for t in (seg.k, seg.v):
+            if t.stride(3) != 1 or t.data_ptr() % 16 != 0:
+                return False
+            if any((s * esize) % 16 != 0 for s in (t.stride(0), t.stride(1), t.stride(2))):
+                return False
+    return True
+
+
+def triton_segmented_q1_attention(
+    q_BxHxD: Tensor,
+    segments: list[KVSegment],
+    *,
+    extra_kv: list[tuple[Tensor, Tensor]] | None = None,
+    attn_dtype: torch.dtype,
+) -> Optional[Tensor]:
+    """One query per (batch, head) over <= 3 segments plus <= 2 always-visible extra keys.
+
+    Returns fp32 [B, H, D], or None when the inputs are outside what the kernel supports (the
+    reference's contract: the caller then falls back).
+    """
+    if not q_BxHxD.is_cuda:
+        return None
+    if len(segments) > 3:
+        return None
+    if extra_kv is not None and len(extra_kv) > 2:
+        return None
+    batch_size, n_head, head_dim = q_BxHxD.shape
+    if head_dim not in _DECODE_HEAD_DIMS:
+        return None
+    if any((not seg.k.is_cuda) or (not seg.v.is_cuda) for seg in segments):
+        return None
+    if any((not seg.k.is_contiguous()) or (not seg.v.is_contiguous()) for seg in segments):
+        return None
+    if not _segments_compatible(segments, batch_size, n_head, head_dim, q_BxHxD.device):
+        return None
+    extras = []
+    for ek, ev in extra_kv or []:
+        extras.append(
+            (ek.to(attn_dtype).float().contiguous().expand(batch_size, n_head, head_dim).contiguous(),
+             ev.to(attn_dtype).float().contiguous().expand(batch_size, n_head, head_dim).contiguous())
+        )
+    q32 = q_BxHxD.to(attn_dtype).float().contiguous().view(batch_size, 1, n_head, head_dim)
+    out = torch.empty((batch_size, n_head, head_dim), device=q_BxHxD.device, dtype=torch.float32)
+    out4 = out.view(batch_size, 1, n_head, head_dim)
+    _run_decode(q32, 1, list(segments), extras, [1] * len(extras), out4)
+    return out
+
+
+def triton_segmented_q2_attention(
+    q_Bx2xHxD: Tensor,
+    segments: list[KVSegment],
+    *,
+    current_normal_k_BxHxD: Tensor,
+    current_normal_v_BxHxD: Tensor,
+    current_predict_k_BxHxD: Tensor,
+    current_predict_v_BxHxD: Tensor,
+    attn_dtype: torch.dtype,
+) -> Tensor:
+    """Two queries per (batch, head): slot 0 (input) sees the segments + current input key; slot 1
+    (<predict>) additionally sees the current <predict> key. Fail-fast: raises RuntimeError on any
+    unsupported input, as the reference does. Returns fp32 [B, 2, H, D]."""
+    if not q_Bx2xHxD.is_cuda:
+        raise RuntimeError("CUDA tensors are required for SPS-family cached generation attention")
+    if len(segments) > 2:
+        raise RuntimeError(f"SPS-family q2 attention supports at most 2 segments, got {len(segments)}")
+    batch_size, n_slots, n_head, head_dim = q_Bx2xHxD.shape
+    if n_slots != 2:
+        raise RuntimeError(f"Expected q_Bx2xHxD slot dimension to be 2, got {n_slots}")
+    if head_dim <= 0 or head_dim > 256:
+        raise RuntimeError(f"Unsupported SPS-family q2 attention head_dim={head_dim}")
+    if head_dim not in _DECODE_HEAD_DIMS:
+        raise RuntimeError(f"sps_amd q2 attention is built for head_dim in {_DECODE_HEAD_DIMS}, got {head_dim}")
+    current = [current_normal_k_BxHxD, current_normal_v_BxHxD, current_predict_k_BxHxD, current_predict_v_BxHxD]
+    for tensor in current:
+        if not tensor.is_cuda:
+            raise RuntimeError("Current-token K/V tensors must be CUDA tensors")
+        if tensor.shape != (batch_size, n_head, head_dim):
+            raise RuntimeError(
+                "Current-token K/V tensors must have shape "
+                f"{(batch_size, n_head, head_dim)}, got {tuple(tensor.shape)}"
+            )
+    for seg in segments:
+        if seg.k.dim() != 4 or seg.v.dim() != 4:
+            raise RuntimeError("Segment K/V tensors must be rank-4 [B,H,T,D]")
+        if seg.k.shape != seg.v.shape:
+            raise RuntimeError(f"Segment K/V shapes differ: {tuple(seg.k.shape)} vs {tuple(seg.v.shape)}")
+        if seg.k.size(0) != batch_size or seg.k.size(1) != n_head or seg.k.size(3) != head_dim:
+            raise RuntimeError(
+                "Segment K/V tensors must match query batch/head/head_dim, got "
+                f"{tuple(seg.k.shape)} for query {(batch_size, n_head, head_dim)}"
+            )
+        if (not seg.k.is_cuda) or (not seg.v.is_cuda):
+            raise RuntimeError("Segment K/V tensors must be CUDA tensors")
+        if (not seg.k.is_contiguous()) or (not seg.v.is_contiguous()):
+            raise RuntimeError("Segment K/V tensors must be contiguous")
+        if seg.lengths.device != q_Bx2xHxD.device:
+            raise RuntimeError("Segment lengths must live on the same device as query")
+        _segment_scan_len(seg)
+    if not _segments_compatible(segments, batch_size, n_head, head_dim, q_Bx2xHxD.device):
+        raise RuntimeError("sps_amd q2 attention: segments must share a bf16/f16/f32 dtype, int lengths "
+                           "of shape [B] or [B, H] and 16-byte aligned rows")
+    extras = [
+        (current_normal_k_BxHxD.to(attn_dtype).float().contiguous(),
+         current_normal_v_BxHxD.to(attn_dtype).float().contiguous()),
+        (current_predict_k_BxHxD.to(attn_dtype).float().contiguous(),
+         current_predict_v_BxHxD.to(attn_dtype).float().contiguous()),
+    ]
+    q32 = q_Bx2xHxD.to(attn_dtype).float().contiguous()
+    out = torch.empty((batch_size, 2, n_head, head_dim), device=q_Bx2xHxD.device, dtype=torch.float32)
+    return _run_decode(q32, 2, list(segments), extras, [0b11, 0b10], out)
+
+
+def masked_kv_attention(
+    q_BxHxD: Tensor,
+    segments: list[KVSegment],
+    *,
+    extra_kv: list[tuple[Tensor, Tensor]] | None = None,
+    attn_dtype: torch.dtype,
+    check_finite: bool = False,
+    error_context: str = "",
+    prefer_triton: bool = False,
+    require_triton: bool = False,
+) -> Tensor:
+    """Attention of one query per (batch, head) over variable-length KV segments plus extra keys.
+
+    Same contract as the reference (decode_attention.py:597-704): fp32 [B, H, D] output, zeros when
+    there is no key at all, RuntimeError on an empty row / non-finite input when ``check_finite``.
+    ``prefer_triton`` / ``require_triton`` are accepted for compatibility; every call runs the HIP
+    kernel. A row with no attended key yields 0 (the reference's padded-SDPA path yields NaN there).
+    """
+    del prefer_triton
+    if not q_BxHxD.is_cuda:
+        raise RuntimeError(f"sps_amd masked_kv_attention runs on the GPU only{error_context}")
+    b, n_head, head_dim = q_BxHxD.shape
+    n_extra = len(extra_kv) if extra_kv else 0
+    if check_finite:
+        seg_maxlens = [
+            0 if seg.lengths.numel() == 0 else min(int(seg.lengths.max().item()), _segment_scan_len(seg))
+            for seg in segments
+        ]
+        total_len = sum(seg_maxlens) + n_extra
+        if total_len == 0:
+            return q_BxHxD.new_zeros((b, n_head, head_dim), dtype=torch.float32)
+        counts = torch.full((b, n_head), n_extra, device=q_BxHxD.device, dtype=torch.long)
+        for seg, max_len in zip(segments, seg_maxlens):
+            if max_len == 0:
+                continue
+            ln = seg.lengths.clamp(min=0, max=max_len).long()
+            counts = counts + (ln.view(b, 1).expand(b, n_head) if ln.dim() == 1 else ln)
+        if bool((counts <= 0).any()):
+            raise RuntimeError(f"Invalid mask with no valid keys{error_context}")
+        finite = bool(torch.isfinite(q_BxHxD).all())
+        for seg, max_len in zip(segments, seg_maxlens):
+            if max_len:
+                finite = finite and bool(torch.isfinite(seg.k[:, :, :max_len]).all())
+                finite = finite and bool(torch.isfinite(seg.v[:, :, :max_len]).all())
+        for ek, ev in extra_kv or []:
+            finite = finite and bool(torch.isfinite(ek).all()) and bool(torch.isfinite(ev).all())
+        if not finite:
+            raise RuntimeError(f"Non-finite QKV{error_context}")
+    out = triton_segmented_q1_attention(q_BxHxD, segments, extra_kv=extra_kv, attn_dtype=attn_dtype)
+    if out is None:
+        if require_triton:
+            raise RuntimeError(f"Triton segmented q1 attention is required but unavailable{error_context}")
+        raise RuntimeError(f"sps_amd masked_kv_attention: unsupported inputs (no fallback path){error_context}")
+    if check_finite and not bool(torch.isfinite(out).all()):
+        raise RuntimeError(f"Non-finite attention output{error_context}")
+    return out

@@ -1,0 +1,239 @@
+"""Parity of the HIP attention kernels with the CPU oracle (GPU).
+
+Bar: masks bit-exact; bf16/f16 outputs and gradients within
+max-abs 2e-2 / rel 1e-2 of the float64 oracle evaluated on the same (16-bit) inputs.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import mask as M
+from sps_amd import attention as SA
+from sps_amd import _native as N
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+FAMILY = {"full": N.FAMILY_FULL, "sps": N.FAMILY_SPS, "reverse_sps": N.FAMILY_REVERSE_SPS}
+API = {
+    "full": lambda q, k, v, s, w, d, p: SA.full_attention(q, k, v, s, documents_idx_BxT=d),
+    "sps": lambda q, k, v, s, w, d, p: SA.sps_sliding_attention(q, k, v, s, w, documents_idx_BxT=d,
+                                                                  persistent_key_window=p),
+    "reverse_sps": lambda q, k, v, s, w, d, p: SA.reverse_sps_sliding_attention(
+        q, k, v, s, w, documents_idx_BxT=d, persistent_key_window=p),
+}
+
+
+def _packed_docs(rng, b, tokens, family, max_len=None):
+    rows = []
+    for _ in range(b):
+        row, fill, i = [], 0, 0
+        while fill < tokens:
+            ln = int(rng.integers(1, max_len or max(2, tokens // 2)))
+            ln = min(ln, tokens - fill)
+            row += [i] * ln
+            fill += ln
+            i += 1
+        rows.append(row)
+    ids = np.array(rows, dtype=np.int64)
+    return ids if family == "full" else np.repeat(ids, 2, axis=1)
+
+
+def _check(family, b, h, n, d, window=0, docs=None, pkw=None, dtype=torch.bfloat16, seed=0, layout="bhnd",
+           grads=True, docs_dtype=torch.int64):
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(seed)
+    shape = (b, n, h, d) if layout == "bnhd" else (b, h, n, d)
+    q, k, v, do = (torch.randn(shape, generator=g).to(dtype) for _ in range(4))
+    if layout == "bnhd":
+        q, k, v, do = (t.transpose(1, 2) for t in (q, k, v, do))
+    scale = 1.0 / math.sqrt(d)
+    docs_t = None if docs is None else torch.tensor(docs, dtype=docs_dtype, device=dev)
+    qg, kg, vg = (t.to(dev).requires_grad_(grads) for t in (q, k, v))
+    out = API[family](qg, kg, vg, scale, window, docs_t, pkw)
+    mask = M.batch_mask(FAMILY[family], docs, n=n, window=window, pkw=pkw, batch=b)
+    qn, kn, vn, don = (t.float().numpy() for t in (q, k, v, do))
+    o_ref, _ = A.forward(qn, kn, vn, mask, scale)
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(o_ref).float(), atol=ATOL, rtol=RTOL)
+    if grads:
+        out.backward(do.to(dev))
+        dq, dk, dv = A.backward(qn, kn, vn, don, mask, scale)
+        for name, got, want in (("dq", qg.grad, dq), ("dk", kg.grad, dk), ("dv", vg.grad, dv)):
+            torch.testing.assert_close(got.float().cpu(), torch.from_numpy(want).float(), atol=ATOL, rtol=RTOL,
+                                       msg=lambda m, name=name: f"{name}: {m}")
+
+
+@pytest.mark.parametrize("family", ["sps", "reverse_sps"])
+@pytest.mark.parametrize("has_docs", [False, True])
+def test_reference_kernel_test_shape(family, has_docs):
+    # attention/triton/test_sps_attention.py:79-131: B1 H2 T16 D64, w=3, seed 17, docs [0*6,1*8,2*2].
+    docs = None
+    if has_docs:
+        docs = np.repeat(np.array([[0] * 6 + [1] * 8 + [2] * 2]), 2, axis=1)
+    _check(family, 1, 2, 32, 64, window=3, docs=docs, seed=17)
+
+
+@pytest.mark.parametrize("family", ["sps", "reverse_sps"])
+def test_persistent_key_window_reference_config(family):
+    # models/attention/test_persistent_key_window.py:62-98: n_ctx 8, D 64, fp16, window 8, pkw 1.
+    _check(family, 1, 1, 8, 64, window=8, pkw=1, dtype=torch.float16, grads=True)
+
+
+CASES = [
+    # family, b, h, n, d, window, docs, pkw, dtype, layout
+    ("full", 2, 3, 200, 64, 0, "packed", None, torch.bfloat16, "bhnd"),
+    ("full", 1, 2, 512, 128, 0, None, None, torch.bfloat16, "bnhd"),
+    ("full", 1, 2, 300, 32, 0, "random", None, torch.float16, "bhnd"),
+    ("sps", 2, 2, 512, 64, 64, "packed", None, torch.bfloat16, "bnhd"),
+    ("sps", 1, 2, 1030, 64, 64, "packed", None, torch.bfloat16, "bhnd"),
+    ("sps", 1, 1, 768, 64, 0, None, None, torch.bfloat16, "bhnd"),
+    ("sps", 1, 2, 400, 128, 5000, "packed", None, torch.bfloat16, "bhnd"),
+    ("sps", 2, 1, 260, 16, 7, "random", 3, torch.float16, "bhnd"),
+    ("sps", 1, 2, 512, 32, 33, "packed", 0, torch.bfloat16, "bnhd"),
+    ("reverse_sps", 2, 2, 512, 64, 64, "packed", None, torch.bfloat16, "bhnd"),
+    ("reverse_sps", 1, 2, 340, 128, 17, None, 40, torch.float16, "bnhd"),
+    ("reverse_sps", 1, 1, 200, 64, -1, "packed", None, torch.bfloat16, "bhnd"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-n{c[3]}-d{c[4]}-w{c[5]}-{c[6]}-pkw{c[7]}" for c in CASES])
+def test_parity_matrix(case):
+    family, b, h, n, d, w, docs_kind, pkw, dtype, layout = case
+    rng = np.random.default_rng(n + d)
+    tokens = n if family == "full" else n // 2
+    docs = None
+    if docs_kind == "packed":
+        docs = _packed_docs(rng, b, tokens, family)
+    elif docs_kind == "random":
+        docs = rng.integers(0, 3, size=(b, n)).astype(np.int64)
+    _check(family, b, h, n, d, window=w, docs=docs, pkw=pkw, dtype=dtype, layout=layout, seed=n)
+
+
+def test_int32_documents():
+    rng = np.random.default_rng(1)
+    docs = _packed_docs(rng, 2, 160, "sps")
+    _check("sps", 2, 2, 320, 64, window=9, docs=docs, docs_dtype=torch.int32)
+
+
+MASK_CASES = [
+    ("sps", 512, 64, "packed", None),
+    ("sps", 300, 5, "random", None),
+    ("sps", 256, 0, None, 2),
+    ("reverse_sps", 512, 64, "packed", 7),
+    ("reverse_sps", 130, 3, "random", -1),
+    ("full", 333, 0, "packed", None),
+    ("full", 256, 0, "random", None),
+    ("sps", 1024, 4096, "packed", None),
+]
+
+
+@pytest.mark.parametrize("schedule", [0, 1])
+@pytest.mark.parametrize("case", MASK_CASES, ids=[f"{c[0]}-n{c[1]}-w{c[2]}-{c[3]}-pkw{c[4]}" for c in MASK_CASES])
+def test_mask_bit_exact(case, schedule):
+    # The block schedule + tile classification + per-element predicate of the kernels, materialised
+    # by sps_attn_mask, equals the oracle predicate on every (query, key) pair.
+    family, n, w, docs_kind, pkw = case
+    rng = np.random.default_rng(n + w)
+    b = 2
+    tokens = n if family == "full" else n // 2
+    docs = None
+    if docs_kind == "packed":
+        docs = _packed_docs(rng, b, tokens, family, max_len=90)
+    elif docs_kind == "random":
+        docs = rng.integers(0, 4, size=(b, n)).astype(np.int64)
+    docs_t = None if docs is None else torch.tensor(docs, device="cuda")
+    got = SA.attention_mask(FAMILY[family], n, docs_t, batch=b, window=w, persistent_key_window=pkw,
+                            schedule=schedule).cpu().numpy().astype(bool)
+    want = M.batch_mask(FAMILY[family], docs, n=n, window=w, pkw=pkw, batch=b)
+    assert (got == want).all(), f"{int((got != want).sum())} mismatching pairs"
+
+
+@pytest.mark.parametrize("family", ["sps", "full"])
+def test_visible_count_through_forward_kernel(family):
+    # Q = K = 0 makes every visible score equal, so the forward kernel's LSE is log2(#visible keys):
+    # an end-to-end check of the mask the real kernel applies, row by row, at a C3-like length.
+    n, b, h, d = 4096, 2, 2, 64
+    rng = np.random.default_rng(5)
+    tokens = n if family == "full" else n // 2
+    docs = _packed_docs(rng, b, tokens, family, max_len=900)
+    z = torch.zeros((b, h, n, d), dtype=torch.bfloat16, device="cuda")
+    v = torch.randn((b, h, n, d), device="cuda").to(torch.bfloat16)
+    _, lse, *_ = SA.attention_forward(z, z, v, 0.125, FAMILY[family], 64, torch.tensor(docs, device="cuda"))
+    counts = torch.round(torch.exp2(lse.double())).long().cpu().numpy()
+    for bi in range(b):
+        want = M.mask_c(FAMILY[family], n, docs[bi], 64).sum(axis=1)
+        for hi in range(h):
+            assert (counts[bi, hi] == want).all()
+
+
+def test_full_size_c3_heads_against_oracle():
+    # C3 shape (N = 4096, w = 64, packed log-normal documents) checked head by head against the
+    # oracle for a subset of (batch, head) pairs, forward and backward.
+    from sps_amd.workloads import C3, make_qkv, position_doc_ids
+
+    ids, _ = position_doc_ids(C3, seed=0)
+    q, k, v, do = make_qkv(C3, seed=0)
+    sel_b, sel_h = [0, 3], [0, 15]
+    dev = torch.device("cuda")
+    qg, kg, vg = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+    docs = torch.tensor(ids, device=dev)
+    out = SA.sps_sliding_attention(qg, kg, vg, 0.125, 64, documents_idx_BxT=docs)
+    out.backward(do.to(dev))
+    for bi in sel_b:
+        mask = M.batch_mask(N.FAMILY_SPS, ids[bi:bi + 1], window=64)
+        for hi in sel_h:
+            sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+            qn, kn, vn, don = (t[sl].float().numpy() for t in (q, k, v, do))
+            o_ref, _ = A.forward(qn, kn, vn, mask, 0.125)
+            dq, dk, dv = A.backward(qn, kn, vn, don, mask, 0.125)
+            torch.testing.assert_close(out[sl].float().cpu(), torch.from_numpy(o_ref).float(), atol=ATOL, rtol=RTOL)
+            for got, want in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
+                torch.testing.assert_close(got[sl].float().cpu(), torch.from_numpy(want).float(), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("family", ["full", "reverse_sps"])
+def test_no_cross_document_leakage(family):
+    # attention/triton/test_document_leakage.py: poison document 2's K/V with NaN; document 1's
+    # outputs stay finite and equal a solo run on document 1.
+    torch.manual_seed(2024)
+    dev = "cuda"
+    b, h, n, d = 1, 2, 256, 64
+    half = n // 2
+    q, k, v = (torch.randn(b, h, n, d, device=dev, dtype=torch.bfloat16) for _ in range(3))
+    fn = API[family]
+    solo = fn(q[:, :, :half], k[:, :, :half], v[:, :, :half], 1 / 8, 4, None, None)
+    kp, vp = k.clone(), v.clone()
+    kp[:, :, half:] = float("nan")
+    vp[:, :, half:] = float("nan")
+    docs = torch.zeros((b, n), dtype=torch.int64, device=dev)
+    docs[:, half:] = 1
+    out = fn(q, kp, vp, 1 / 8, 4, docs, None)
+    assert torch.isfinite(out[:, :, :half]).all()
+    torch.testing.assert_close(out[:, :, :half].float(), solo.float(), atol=2e-2, rtol=1e-2)
+
+
+def test_strided_and_contiguous_inputs_agree():
+    g = torch.Generator().manual_seed(3)
+    b, h, n, d = 2, 4, 384, 64
+    base = torch.randn((b, n, 3 * h * d), generator=g).to(torch.bfloat16).cuda()
+    q, k, v = base.split(h * d, dim=2)
+    q, k, v = (t.view(b, n, h, d).transpose(1, 2) for t in (q, k, v))  # the model's views
+    docs = torch.tensor(np.repeat(np.array([[0] * 100 + [1] * 92] * b), 2, axis=1), device="cuda")
+    o1 = SA.sps_sliding_attention(q, k, v, 0.125, 16, documents_idx_BxT=docs)
+    o2 = SA.sps_sliding_attention(q.contiguous(), k.contiguous(), v.contiguous(), 0.125, 16, documents_idx_BxT=docs)
+    torch.testing.assert_close(o1, o2, atol=0, rtol=0)
+    assert o1.transpose(1, 2).is_contiguous()
+
+
+def test_reference_assertions_preserved():
+    q = torch.randn(1, 1, 30, 64, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        SA.sps_sliding_attention(q[:, :, :29], q[:, :, :29], q[:, :, :29], 0.125, 3)
+    with pytest.raises(AssertionError):
+        SA.sps_sliding_attention(q, q, q, 0.125, 3, documents_idx_BxT=torch.zeros(1, 28, dtype=torch.long, device="cuda"))
+    with pytest.raises(AssertionError):
+        SA.full_attention(q[..., :48], q[..., :48], q[..., :48], 0.125)

@@ -1,0 +1,102 @@
+"""The C-ABI library loads, exports what include/sps_attn.h declares, and validates arguments
+before touching the GPU (CPU-only: every call here fails validation, so no kernel is launched)."""
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from sps_amd import _native as N
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "sps_attn.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sps_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declarations_match_binding():
+    assert _declared_functions() == sorted(N.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.sps_version().startswith(b"sps_attn")
+
+
+def _fwd(**over):
+    args = dict(family=1, B=1, H=1, N=64, D=64, dtype=N.DTYPE_BF16, sm_scale=0.125, window=4, has_pkw=0, pkw=-1,
+                docs=None, docs_dtype=N.DTYPE_I64, ws=None, ws_bytes=0, ptr=0x10000, strides=(64 * 64, 64 * 64, 64))
+    args.update(over)
+    st = N.i64_array(args["strides"])
+    p = args["ptr"]
+    lse = 0x20000
+    return N.lib().sps_attn_fwd(
+        args["family"], args["B"], args["H"], args["N"], args["D"], args["dtype"],
+        p, st, p, st, p, st, p, st, lse, args["docs"], args["docs_dtype"], 0,
+        args["sm_scale"], args["window"], args["has_pkw"], args["pkw"], args["ws"], args["ws_bytes"], None,
+    )
+
+
+@pytest.mark.parametrize(
+    "over,code,needle",
+    [
+        (dict(family=7), N.SPS_E_INVALID, "family"),
+        (dict(N=63), N.SPS_E_INVALID, "even"),
+        (dict(D=256), N.SPS_E_UNSUPPORTED, "head_dim"),
+        (dict(D=48), N.SPS_E_UNSUPPORTED, "head_dim"),
+        (dict(dtype=N.DTYPE_F32), N.SPS_E_UNSUPPORTED, "dtype"),
+        (dict(sm_scale=0.0), N.SPS_E_UNSUPPORTED, "sm_scale"),
+        (dict(sm_scale=float("nan")), N.SPS_E_UNSUPPORTED, "sm_scale"),
+        (dict(ptr=0x10008), N.SPS_E_INVALID, "aligned"),
+        (dict(strides=(64 * 64, 64 * 64, 60)), N.SPS_E_INVALID, "multiple of 8"),
+        (dict(docs=0x30000, docs_dtype=N.DTYPE_F32), N.SPS_E_INVALID, "int32 or int64"),
+        (dict(docs=0x30000, docs_dtype=N.DTYPE_I64, ws_bytes=0), N.SPS_E_WORKSPACE, "workspace"),
+    ],
+)
+def test_forward_argument_validation(over, code, needle):
+    assert _fwd(**over) == code
+    assert needle in N.last_error()
+
+
+def test_empty_problem_is_a_noop():
+    assert _fwd(B=0) == N.SPS_OK
+    assert _fwd(N=0) == N.SPS_OK
+
+
+def test_workspace_sizes():
+    lib = N.lib()
+    assert lib.sps_attn_workspace_bytes(1, 4, 16, 4096, 0, 0) == 0
+    with_docs = lib.sps_attn_workspace_bytes(1, 4, 16, 4096, 1, 0)
+    assert with_docs >= 2 * 4 * (4096 // 32) * 8
+    bwd = lib.sps_attn_workspace_bytes(1, 4, 16, 4096, 1, 1)
+    assert bwd >= with_docs + 4 * 16 * 4096 * 4
+    scans = N.i64_array([64, 4096])
+    dec = lib.sps_decode_workspace_bytes(64, 16, 64, 1, N.DTYPE_BF16, 2, scans)
+    assert dec >= 64 * 16 * (1 + 16) * (64 + 4) * 4
+
+
+def test_decode_argument_validation():
+    lib = N.lib()
+    z = N.i64_array([0, 0, 0])
+    rc = lib.sps_decode(1, 1, 64, 3, 0x1000, z, N.DTYPE_BF16, 0, None, z, None, z, None, None, None, z,
+                        0, None, None, z, None, 0.125, 0x2000, z, None, 0, None)
+    assert rc == N.SPS_E_INVALID and "nq" in N.last_error()
+    rc = lib.sps_decode(1, 1, 48, 1, 0x1000, z, N.DTYPE_BF16, 0, None, z, None, z, None, None, None, z,
+                        0, None, None, z, None, 0.125, 0x2000, z, None, 0, None)
+    assert rc == N.SPS_E_UNSUPPORTED
+    rc = lib.sps_decode(1, 1, 64, 1, 0x1000, z, N.DTYPE_BF16, 4, None, z, None, z, None, None, None, z,
+                        0, None, None, z, None, 0.125, 0x2000, z, None, 0, None)
+    assert rc == N.SPS_E_INVALID and "segments" in N.last_error()
+
+
+def test_last_error_truncates():
+    _fwd(family=9)
+    buf = C.create_string_buffer(8)
+    full = N.lib().sps_last_error(buf, len(buf))
+    assert full > 7 and len(buf.value) == 7
