@@ -1,0 +1,341 @@
+#!/usr/bin/env python3
+"""Benchmark of the SPS attention hot path on one MI355X.
+
+Headline (``value``): C3 — SPS sliding-window attention (w = 64) forward + backward, bf16, B 4, H 16,
+D 64, 4096 interleaved positions, rows packed with log-normal documents — in useful TFLOP/s
+(14 * D * visible pairs per step: 4 * D forward, 10 * D backward, the reference's 2.5x convention of
+original_flash_attn.py:749-755). A step is one forward and one backward over the whole batch, with
+inputs resident in HBM. Also reported: C5 segmented decode (µs/step, GB/s), the roofline of the
+dominant kernel of each (timed live with HIP events on the launch stream), and the reference's CPU
+path timed on this host on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps S] [--no-cpu-baseline]
+Prints one JSON line on stdout (progress goes to stderr).
+"""
+
+from __future__ import annotations
+
+import argparse
+import functools
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "SPS w=64 attn fwd+bwd TFLOP/s @4096 pos; segmented decode µs/step + GB/s"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+# ----------------------------------------------------------------------------------------------
+# Prefill / training: C3
+# ----------------------------------------------------------------------------------------------
+def bench_attention(cfg, steps: int, warmup: int):
+    import torch
+
+    from sps_amd import _native as N
+    from sps_amd import attention as SA
+    from sps_amd.workloads import make_qkv, position_doc_ids, useful_flops, visible_pairs
+
+    family = {"full": N.FAMILY_FULL, "sps": N.FAMILY_SPS, "reverse_sps": N.FAMILY_REVERSE_SPS}[cfg.family]
+    ids, lengths = position_doc_ids(cfg, seed=0)
+    q, k, v, do = (t.cuda() for t in make_qkv(cfg, seed=0))
+    docs = torch.tensor(ids, device="cuda")
+    scale = 1.0 / math.sqrt(cfg.head_dim)
+    pairs = visible_pairs(cfg, lengths) * cfg.heads
+
+    ev = []
+
+    def step(record: bool):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)] if record else None
+        if record:
+            e[0].record()
+        o, lse, *_ = SA.attention_forward(q, k, v, scale, family, cfg.window, docs)
+        if record:
+            e[1].record()
+        SA.attention_backward(do, q, k, v, o, lse, scale, family, cfg.window, docs,
+                              between_passes=(e[2].record if record else None))
+        if record:
+            e[3].record()
+            ev.append(e)
+
+    for _ in range(warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    fwd = [e[0].elapsed_time(e[1]) for e in ev]
+    dq = [e[1].elapsed_time(e[2]) for e in ev]
+    dkdv = [e[2].elapsed_time(e[3]) for e in ev]
+    ms_per_step = wall / steps * 1e3
+    flops = useful_flops(cfg, lengths)
+    d = cfg.head_dim
+    # Algorithmic FLOPs each kernel's formulation performs on the visible pairs (MFMA work):
+    # forward S, PV = 2 products; dQ pass S, dP, dQ = 3; dK/dV pass S, dP, dV, dK = 4.
+    kernels = {
+        "attn_fwd_kernel": {"ms": statistics.mean(fwd), "flop": 4.0 * d * pairs},
+        "attn_bwd_dq_kernel": {"ms": statistics.mean(dq), "flop": 6.0 * d * pairs},
+        "attn_bwd_dkdv_kernel": {"ms": statistics.mean(dkdv), "flop": 8.0 * d * pairs},
+    }
+    for kk in kernels.values():
+        kk["tflops"] = kk["flop"] / (kk["ms"] * 1e-3) / 1e12
+        kk["frac"] = kk["tflops"] / PEAK_BF16_TFLOPS
+    dominant = max(kernels, key=lambda name: kernels[name]["ms"])
+    dk = kernels[dominant]
+    return {
+        "value": flops / (ms_per_step * 1e-3) / 1e12,
+        "ms_per_step": ms_per_step,
+        "device_ms_per_step": statistics.mean(f + a + b for f, a, b in zip(fwd, dq, dkdv)),
+        "useful_gflop_per_step": flops / 1e9,
+        "visible_pairs": pairs,
+        "doc_lengths": lengths,
+        "kernels": {name: {"ms": round(x["ms"], 4), "tflops": round(x["tflops"], 2), "frac": round(x["frac"], 4),
+                           "algorithmic_gflop": round(x["flop"] / 1e9, 3)} for name, x in kernels.items()},
+        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(dk["tflops"], 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dk["frac"], 4), "traffic": None},
+    }
+
+
+def cpu_attention_baseline(cfg, budget_s: float):
+    """Reference CPU path (dense masked SDPA fwd + autograd bwd, fp32) on whole batch rows of the same
+    inputs until `budget_s` seconds are spent (at least one row)."""
+    import torch
+
+    from oracle import cpu_fallback as CF
+    from sps_amd.workloads import make_qkv, position_doc_ids, visible_pairs
+
+    family = {"full": 0, "sps": 1, "reverse_sps": 2}[cfg.family]
+    ids, lengths = position_doc_ids(cfg, seed=0)
+    q, k, v, do = (t.float() for t in make_qkv(cfg, seed=0))
+    scale = 1.0 / math.sqrt(cfg.head_dim)
+    # Warm-up on a short prefix so the timed rows are steady-state.
+    n_w = 256
+    CF.dense_sdpa_fwd_bwd(q[:1, :, :n_w], k[:1, :, :n_w], v[:1, :, :n_w], do[:1, :, :n_w],
+                          CF.mask_from_docs(family, ids[0, :n_w], cfg.window).unsqueeze(0), scale)
+    rows, spent = 0, 0.0
+    while rows < cfg.batch and (rows == 0 or spent < budget_s):
+        mask = CF.mask_from_docs(family, ids[rows], cfg.window).unsqueeze(0)
+        t0 = time.perf_counter()
+        CF.dense_sdpa_fwd_bwd(q[rows:rows + 1], k[rows:rows + 1], v[rows:rows + 1], do[rows:rows + 1], mask, scale)
+        spent += time.perf_counter() - t0
+        rows += 1
+    pairs = visible_pairs(cfg, lengths[:rows]) * cfg.heads
+    flops = 14.0 * cfg.head_dim * pairs
+    return {"value": round(flops / spent / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{rows} of {cfg.batch} batch rows (all {cfg.heads} heads, N={cfg.n}) of the same inputs, "
+                      f"dense masked SDPA fwd+bwd fp32 (the reference's test reference), {spent:.1f} s; "
+                      f"cpu: {cpu_model()}"}
+
+
+# ----------------------------------------------------------------------------------------------
+# Decode: C5
+# ----------------------------------------------------------------------------------------------
+@functools.lru_cache(maxsize=1)
+def _decode_inputs(cfg, seed: int = 0):
+    """C5 inputs drawn once on the CPU (shared by the GPU and CPU legs)."""
+    import torch
+
+    from sps_amd.workloads import decode_lengths
+
+    lengths = decode_lengths(cfg, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    B, H, D = cfg.seqs, cfg.heads, cfg.head_dim
+    q = torch.randn((B, H, D), generator=g).to(torch.bfloat16)
+    rk = torch.randn((B, H, cfg.storage, D), generator=g).to(torch.bfloat16)
+    rv = torch.randn((B, H, cfg.storage, D), generator=g).to(torch.bfloat16)
+    wk = torch.randn((B, H, cfg.ring, D), generator=g).to(torch.bfloat16)
+    wv = torch.randn((B, H, cfg.ring, D), generator=g).to(torch.bfloat16)
+    ck, cv, pk, pv = (torch.randn((B, H, D), generator=g).to(torch.bfloat16) for _ in range(4))
+    ring_len = torch.full((B,), cfg.ring, dtype=torch.int64)
+    ret_len = lengths.view(B, 1).expand(B, H).contiguous()
+    return lengths, q, (wk, wv, ring_len), (rk, rv, ret_len), ((ck, cv), (pk, pv))
+
+
+def bench_decode(cfg, steps: int, warmup: int):
+    import torch
+
+    from sps_amd import decode_attention as DA
+    from sps_amd.workloads import decode_bytes
+
+    lengths, q, ring, ret, extras = _decode_inputs(cfg)
+    dev = "cuda"
+    segs = [DA.KVSegment(ring[0].to(dev), ring[1].to(dev), ring[2].to(dev), max_len_cap=cfg.ring),
+            DA.KVSegment(ret[0].to(dev), ret[1].to(dev), ret[2].to(dev), max_len_cap=cfg.storage)]
+    qd = q.to(dev)
+    ex = [(a.to(dev), b.to(dev)) for a, b in extras]
+    # Kernel-level call: the inputs as sps_decode takes them (fp32 query and extras).
+    q32 = qd.float().view(cfg.seqs, 1, cfg.heads, cfg.head_dim).contiguous()
+    ex32 = [(a.float().contiguous(), b.float().contiguous()) for a, b in ex]
+    out = torch.empty((cfg.seqs, 1, cfg.heads, cfg.head_dim), device=dev, dtype=torch.float32)
+
+    def kernel_call():
+        DA._run_decode(q32, 1, segs, ex32, [1, 1], out)
+
+    def api_call():
+        DA.masked_kv_attention(qd, segs, extra_kv=ex, attn_dtype=torch.bfloat16, prefer_triton=True)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        evs = []
+        for _ in range(steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) * 1e3 for a, b in evs]
+
+    k_us = timed(kernel_call)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    a_us = timed(api_call)
+    nbytes = decode_bytes(cfg, lengths, nq=1, n_extra=2, kv_bytes=2)
+    k_med = statistics.median(k_us)
+    gbps = nbytes / (k_med * 1e-6) / 1e9
+    return {
+        "workload": "C5 segmented decode: 64 sequences, 16 heads, D 64, retained U[512,4096] (seed 0), "
+                    "ring 64, 1 <predict> query (ring + retained + current input + current <predict>)",
+        "us_per_step": round(k_med, 3),
+        "api_us_per_step": round(statistics.median(a_us), 3),
+        "gbps": round(gbps, 1),
+        "algorithmic_bytes": nbytes,
+        "roofline": {"kernel": "decode_partial_kernel + decode_merge_kernel", "bound": "hbm",
+                     "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None},
+        "_api_wall_s": time.perf_counter() - t0,
+    }
+
+
+def cpu_decode_baseline(cfg, budget_s: float):
+    import torch
+
+    from oracle import cpu_fallback as CF
+    from sps_amd.workloads import decode_bytes
+
+    lengths, q, ring, ret, extras = _decode_inputs(cfg)
+    segs = [(ring[0], ring[1], ring[2], cfg.ring), (ret[0], ret[1], ret[2], cfg.storage)]
+    ex = [(a.float(), b.float()) for a, b in extras]
+    segs32 = [(a.float(), b.float(), ln, cap) for a, b, ln, cap in segs]
+    qf = q.float()
+    CF.padded_masked_kv_attention(qf, segs32, ex)  # warm-up
+    times = []
+    while len(times) < 3 or (sum(times) < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        CF.padded_masked_kv_attention(qf, segs32, ex)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    nbytes = decode_bytes(cfg, lengths, nq=1, n_extra=2, kv_bytes=2)
+    return {"value": round(med * 1e6, 1), "unit": "us/step", "gbps": round(nbytes / med / 1e9, 3),
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the full C5 step ({len(times)} steps, median) through the reference's padded-SDPA "
+                      f"masked_kv_attention fallback in fp32; cpu: {cpu_model()}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=200)
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work per baseline leg")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every (batch, head) and every "
+              "decode sequence is independent; see DESIGN.md for how it would shard). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (MI355X); none is visible", file=sys.stderr)
+        return 1
+    from sps_amd import _native
+    from sps_amd.workloads import C3, C5
+
+    _native.lib()
+    log(f"C3 fwd+bwd: {args.warmup} warm-up + {args.steps} timed steps")
+    att = bench_attention(C3, args.steps, args.warmup)
+    log(f"C3: {att['value']:.1f} TFLOP/s, {att['ms_per_step']:.3f} ms/step, kernels {att['kernels']}")
+    dec = None
+    if not args.no_decode:
+        log(f"C5 decode: {args.decode_steps} timed steps")
+        dec = bench_decode(C5, args.decode_steps, 20)
+        dec.pop("_api_wall_s")
+        log(f"C5: {dec['us_per_step']} us/step, {dec['gbps']} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (C3 sample)")
+        cpu = cpu_attention_baseline(C3, args.cpu_budget)
+        log(f"CPU C3: {cpu}")
+        if dec is not None:
+            log("CPU baseline (C5)")
+            dec["cpu_baseline"] = cpu_decode_baseline(C5, args.cpu_budget)
+            log(f"CPU C5: {dec['cpu_baseline']}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(att["value"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(att["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: Q/K/V/dO ~ N(0,1) from torch.Generator seed 0; rows packed with log-normal documents "
+                "(median 400 tokens, sigma 0.8, clip [16, 2048], seed 0)",
+        "config": {"workload": "C3 SPS sliding-window attention fwd+bwd (w=64)", "batch": C3.batch,
+                   "heads": C3.heads, "head_dim": C3.head_dim, "positions": C3.n, "window": C3.window,
+                   "useful_gflop_per_step": round(att["useful_gflop_per_step"], 3),
+                   "device_ms_per_step": round(att["device_ms_per_step"], 4)},
+        "kernels": att["kernels"],
+        "roofline": att["roofline"],
+        "cpu_baseline": cpu,
+        "decode": dec,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

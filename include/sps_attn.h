@@ -104,6 +104,34 @@ int sps_attn_bwd(int family, int B, int H, int N, int D, int dtype,
                  float sm_scale, int window, int has_pkw, int pkw,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* Passes of the backward (sps_attn_bwd runs SPS_BWD_DQ, then SPS_BWD_DKDV, on one stream). */
+#define SPS_BWD_DQ 1   /* Delta = rowsum(o * dO) into the workspace, and dq
+                          (reference: _attn_bwd_preprocess + _sps_bwd_dq_kernel,
+                          triton_reverse_sps_flash_attention.py:334-348, triton_sps_flash_attention.py:385-488) */
+#define SPS_BWD_DKDV 2 /* dk, dv from the Delta and document ranges the SPS_BWD_DQ pass left in the workspace
+                          (reference: _sps_bwd_dkdv_kernel, triton_sps_flash_attention.py:272-382) */
+
+/*
+ * One pass of sps_attn_bwd, same arguments plus `pass` (SPS_BWD_DQ or SPS_BWD_DKDV). The SPS_BWD_DKDV
+ * pass must follow an SPS_BWD_DQ pass with the same workspace on the same stream; arguments the pass
+ * does not touch (dk, dv for SPS_BWD_DQ; dq for SPS_BWD_DKDV) are still validated. Lets a caller time
+ * or schedule the two kernels separately, as the reference launches them separately
+ * (triton_sps_flash_attention.py:651-707).
+ */
+int sps_attn_bwd_pass(int pass, int family, int B, int H, int N, int D, int dtype,
+                      const void* q, const int64_t* q_strides,
+                      const void* k, const int64_t* k_strides,
+                      const void* v, const int64_t* v_strides,
+                      const void* o, const int64_t* o_strides,
+                      const void* dout, const int64_t* dout_strides,
+                      const float* lse,
+                      void* dq, const int64_t* dq_strides,
+                      void* dk, const int64_t* dk_strides,
+                      void* dv, const int64_t* dv_strides,
+                      const void* docs, int docs_dtype, int64_t docs_stride_b,
+                      float sm_scale, int window, int has_pkw, int pkw,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /*
  * Writes into mask ([B, N, N] uint8, zero-filled by the caller) a 1 for every (query, key) pair
  * that the attention kernels treat as visible, following the block schedule of the

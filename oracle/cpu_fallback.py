@@ -1,0 +1,92 @@
+"""CPU restatement of the reference's own CPU attention paths — TEST INFRASTRUCTURE ONLY.
+
+Used only by bench.py's ``cpu_baseline`` leg (timed on the GPU box's host cores) and by tests that
+check it against the numpy oracle. Never imported by the product (``sps_amd``).
+
+* ``dense_sdpa_fwd_bwd``: the reference's correctness reference for the prefill kernels, an additive
+  mask (0 on visible pairs, -inf elsewhere) fed to ``torch.nn.functional.scaled_dot_product_attention``
+  in fp32, with the backward from autograd (src/modeling/tests/attention/triton/
+  test_sps_attention.py:25-73, test_full_flash_attention.py:29-59). The dense SPS forward of the
+  reference has no CPU path of its own (src/modeling/models/sps/core.py:63-67), so this is the CPU
+  form of that computation the reference ships.
+* ``padded_masked_kv_attention``: the CPU fallback of ``masked_kv_attention``
+  (src/modeling/models/utils/decode_attention.py:637-698): every segment is cut to its largest live
+  length, segments and the always-visible extra keys are concatenated into one zero-padded K/V
+  tensor with a boolean validity mask, and one SDPA call runs over it in ``attn_dtype``.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+
+def dense_sdpa_fwd_bwd(q, k, v, do, mask_bool, sm_scale):
+    """q, k, v, do: [B, H, N, D] fp32 CPU tensors; mask_bool: [B, N, N] (True = visible).
+
+    Returns (o, dq, dk, dv) in fp32."""
+    qr, kr, vr = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    bias = torch.zeros(mask_bool.shape, dtype=q.dtype)
+    bias.masked_fill_(~mask_bool, float("-inf"))
+    o = F.scaled_dot_product_attention(qr, kr, vr, attn_mask=bias.unsqueeze(1), scale=sm_scale)
+    o.backward(do)
+    return o.detach(), qr.grad, kr.grad, vr.grad
+
+
+def _scan_len(storage: int, max_len_cap) -> int:
+    if storage == 0:
+        return 0
+    if max_len_cap is None:
+        return storage
+    return max(1, min(storage, int(max_len_cap)))
+
+
+def padded_masked_kv_attention(q, segments, extra_kv, attn_dtype=torch.float32):
+    """q: [B, H, D]; segments: list of (k [B,H,S,D], v, lengths [B] or [B,H], max_len_cap);
+    extra_kv: list of (k [B,H,D], v [B,H,D]). Returns fp32 [B, H, D]."""
+    b, h, d = q.shape
+    maxlens = []
+    for (k, _, lengths, cap) in segments:
+        maxlens.append(0 if lengths.numel() == 0 else min(int(lengths.max()), _scan_len(k.shape[2], cap)))
+    total = sum(maxlens) + len(extra_kv)
+    if total == 0:
+        return torch.zeros((b, h, d), dtype=torch.float32)
+    keys = torch.zeros((b, h, total, d), dtype=attn_dtype)
+    vals = torch.zeros_like(keys)
+    valid = torch.zeros((b, h, total), dtype=torch.bool)
+    col = 0
+    for (k, v, lengths, _), n in zip(segments, maxlens):
+        if n == 0:
+            continue
+        keys[:, :, col:col + n] = k[:, :, :n]
+        vals[:, :, col:col + n] = v[:, :, :n]
+        pos = torch.arange(n)
+        lens = lengths.view(b, 1, 1) if lengths.dim() == 1 else lengths.view(b, h, 1)
+        valid[:, :, col:col + n] = pos.view(1, 1, n) < lens
+        col += n
+    for ek, ev in extra_kv:
+        keys[:, :, col] = ek
+        vals[:, :, col] = ev
+        valid[:, :, col] = True
+        col += 1
+    out = F.scaled_dot_product_attention(
+        q.to(attn_dtype).reshape(b * h, 1, d), keys.reshape(b * h, total, d), vals.reshape(b * h, total, d),
+        attn_mask=valid.reshape(b * h, 1, total), scale=1.0 / math.sqrt(d))
+    return out.reshape(b, h, d).float()
+
+
+def mask_from_docs(family: int, docs_row: np.ndarray, window: int) -> torch.Tensor:
+    """[N, N] bool visibility of one batch row, built with torch on the CPU from the predicate of
+    sps_oracle.c (causal, same document, temporary keys within `window` tokens)."""
+    n = docs_row.shape[0]
+    q = torch.arange(n).view(n, 1)
+    k = torch.arange(n).view(1, n)
+    d = torch.as_tensor(docs_row)
+    vis = (k <= q) & (d.view(n, 1) == d.view(1, n))
+    if family != 0:
+        persistent = (k % 2) == (1 if family == 2 else 0)
+        vis &= persistent | ((q // 2 - k // 2) <= window)
+    return vis

@@ -23,6 +23,9 @@ DTYPE_F32 = 2
 DTYPE_I32 = 3
 DTYPE_I64 = 4
 
+BWD_DQ = 1
+BWD_DKDV = 2
+
 FAMILY_FULL = 0
 FAMILY_SPS = 1
 FAMILY_REVERSE_SPS = 2
@@ -33,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "sps_attn_workspace_bytes",
     "sps_attn_fwd",
     "sps_attn_bwd",
+    "sps_attn_bwd_pass",
     "sps_attn_mask",
     "sps_decode_workspace_bytes",
     "sps_decode",
@@ -62,6 +66,16 @@ _SIGNATURES = {
     "sps_attn_bwd": (
         _i32,
         [_i32, _i32, _i32, _i32, _i32, _i32]
+        + [_p, _pi64] * 5
+        + [_p]  # lse
+        + [_p, _pi64] * 3
+        + [_p, _i32, _i64]
+        + [_f32, _i32, _i32, _i32]
+        + [_p, _sz, _p],
+    ),
+    "sps_attn_bwd_pass": (
+        _i32,
+        [_i32, _i32, _i32, _i32, _i32, _i32, _i32]
         + [_p, _pi64] * 5
         + [_p]  # lse
         + [_p, _pi64] * 3

@@ -117,8 +117,12 @@ def attention_forward(q, k, v, sm_scale, family, window=0, documents_idx_BxT=Non
 
 
 def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, documents_idx_BxT=None,
-                       persistent_key_window=None):
-    """Runs the backward kernels; returns (dq, dk, dv) laid out like q, k, v."""
+                       persistent_key_window=None, between_passes=None):
+    """Runs the backward kernels; returns (dq, dk, dv) laid out like q, k, v.
+
+    ``between_passes``: optional callable run on the host after the dQ pass is enqueued and before the
+    dK/dV pass (e.g. to record a torch.cuda.Event on the current stream for per-kernel timing); the two
+    passes are then launched through sps_attn_bwd_pass instead of one sps_attn_bwd call."""
     do = _kernel_view(do)
     b, h, n, d = q.shape
     dq = torch.empty_like(q)
@@ -127,7 +131,7 @@ def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, document
     docs_ptr, docs_code, docs_sb = _docs_args(documents_idx_BxT)
     ws = _workspace(family, b, h, n, documents_idx_BxT is not None, True, q.device)
     has_pkw = persistent_key_window is not None
-    status = N.lib().sps_attn_bwd(
+    args = (
         family, b, h, n, d, _dtype_code(q),
         q.data_ptr(), _strides(q), k.data_ptr(), _strides(k), v.data_ptr(), _strides(v),
         o.data_ptr(), _strides(o), do.data_ptr(), _strides(do), lse.data_ptr(),
@@ -136,7 +140,12 @@ def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, document
         float(sm_scale), int(window), int(has_pkw), int(persistent_key_window) if has_pkw else -1,
         ws.data_ptr(), ws.numel(), _stream(q),
     )
-    N.check("sps_attn_bwd", status)
+    if between_passes is None:
+        N.check("sps_attn_bwd", N.lib().sps_attn_bwd(*args))
+    else:
+        N.check("sps_attn_bwd_pass", N.lib().sps_attn_bwd_pass(N.BWD_DQ, *args))
+        between_passes()
+        N.check("sps_attn_bwd_pass", N.lib().sps_attn_bwd_pass(N.BWD_DKDV, *args))
     return dq, dk, dv
 
 

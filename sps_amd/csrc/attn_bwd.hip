@@ -400,23 +400,26 @@ __global__ __launch_bounds__(256) void mask_dump_kv_kernel(const AttnArgs a) {
 }
 
 template <int D, class E>
-static hipError_t launch_bwd_t(const AttnArgs& a, hipStream_t stream) {
+static hipError_t launch_bwd_t(const AttnArgs& a, int passes, hipStream_t stream) {
   const int nqt = (a.m.N + kTile - 1) / kTile;
   const int64_t nq = (int64_t)nqt * a.B * a.H;
   const int64_t nk = (int64_t)ktiles_per_head(a.m.family, a.m.N) * a.B * a.H;
-  if (nq == 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, E>), dim3((unsigned)nq), dim3(256), 0, stream, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (nk == 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, E>), dim3((unsigned)nk), dim3(256), 0, stream, a);
-  return hipGetLastError();
+  if ((passes & kBwdDq) && nq > 0) {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, E>), dim3((unsigned)nq), dim3(256), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if ((passes & kBwdDkdv) && nk > 0) {
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, E>), dim3((unsigned)nk), dim3(256), 0, stream, a);
+    return hipGetLastError();
+  }
+  return hipSuccess;
 }
 
-hipError_t launch_attn_bwd(const AttnArgs& a, int D, int is_f16, hipStream_t stream) {
-#define SPS_BWD_CASE(DD)                                                                      \
-  case DD:                                                                                    \
-    return is_f16 ? launch_bwd_t<DD, ElemF16>(a, stream) : launch_bwd_t<DD, ElemBF16>(a, stream);
+hipError_t launch_attn_bwd(const AttnArgs& a, int D, int is_f16, int passes, hipStream_t stream) {
+#define SPS_BWD_CASE(DD)                                                                                  \
+  case DD:                                                                                                \
+    return is_f16 ? launch_bwd_t<DD, ElemF16>(a, passes, stream) : launch_bwd_t<DD, ElemBF16>(a, passes, stream);
   switch (D) {
     SPS_BWD_CASE(16)
     SPS_BWD_CASE(32)

@@ -46,7 +46,11 @@ __device__ __forceinline__ int64_t load_doc(const AttnArgs& a, int b, int pos) {
 // Host launchers (each defined next to its kernels). All launches are asynchronous on `stream`.
 hipError_t launch_doc_granules(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_attn_fwd(const AttnArgs& a, int D, int is_f16, hipStream_t stream);
-hipError_t launch_attn_bwd(const AttnArgs& a, int D, int is_f16, hipStream_t stream);
+// Backward passes (bit mask): kBwdDq computes Delta = rowsum(O * dO) and dQ; kBwdDkdv computes dK and dV
+// from the Delta the dQ pass stored.
+constexpr int kBwdDq = 1;
+constexpr int kBwdDkdv = 2;
+hipError_t launch_attn_bwd(const AttnArgs& a, int D, int is_f16, int passes, hipStream_t stream);
 hipError_t launch_mask_dump(const AttnArgs& a, int schedule, hipStream_t stream);
 
 }  // namespace sps

@@ -175,14 +175,16 @@ int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype, const void* 
   return hip_status(sps::launch_attn_fwd(a, D, dtype == SPS_DTYPE_F16, s), "attention forward");
 }
 
-int sps_attn_bwd(int family, int B, int H, int N, int D, int dtype, const void* q, const int64_t* q_strides,
-                 const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
-                 const void* o, const int64_t* o_strides, const void* dout, const int64_t* dout_strides,
-                 const float* lse, void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides,
-                 void* dv, const int64_t* dv_strides, const void* docs, int docs_dtype, int64_t docs_stride_b,
-                 float sm_scale, int window, int has_pkw, int pkw, void* workspace, size_t workspace_bytes,
-                 void* stream) {
+static int attn_bwd_impl(int passes, int family, int B, int H, int N, int D, int dtype, const void* q,
+                         const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                         const int64_t* v_strides, const void* o, const int64_t* o_strides, const void* dout,
+                         const int64_t* dout_strides, const float* lse, void* dq, const int64_t* dq_strides,
+                         void* dk, const int64_t* dk_strides, void* dv, const int64_t* dv_strides, const void* docs,
+                         int docs_dtype, int64_t docs_stride_b, float sm_scale, int window, int has_pkw, int pkw,
+                         void* workspace, size_t workspace_bytes, void* stream) {
   g_last_error.clear();
+  if (passes < 1 || passes > (SPS_BWD_DQ | SPS_BWD_DKDV))
+    return fail(SPS_E_INVALID, "backward pass selector %d is not SPS_BWD_DQ, SPS_BWD_DKDV or both", passes);
   sps::AttnArgs a;
   int rc = setup_common(a, family, B, H, N, docs, docs_dtype, docs_stride_b, window, has_pkw, pkw,
                         workspace, workspace_bytes, 1);
@@ -219,8 +221,43 @@ int sps_attn_bwd(int family, int B, int H, int N, int D, int dtype, const void* 
   a.sm_scale = sm_scale;
   a.scale2 = sm_scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (docs && (rc = hip_status(sps::launch_doc_granules(a, s), "document prepass"))) return rc;
-  return hip_status(sps::launch_attn_bwd(a, D, dtype == SPS_DTYPE_F16, s), "attention backward");
+  // The document ranges are computed by the dQ pass and left in the workspace for the dK/dV pass.
+  if (docs && (passes & SPS_BWD_DQ) && (rc = hip_status(sps::launch_doc_granules(a, s), "document prepass")))
+    return rc;
+  return hip_status(sps::launch_attn_bwd(a, D, dtype == SPS_DTYPE_F16, passes, s), "attention backward");
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int sps_attn_bwd(int family, int B, int H, int N, int D, int dtype, const void* q, const int64_t* q_strides,
+                 const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                 const void* o, const int64_t* o_strides, const void* dout, const int64_t* dout_strides,
+                 const float* lse, void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides,
+                 void* dv, const int64_t* dv_strides, const void* docs, int docs_dtype, int64_t docs_stride_b,
+                 float sm_scale, int window, int has_pkw, int pkw, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  return attn_bwd_impl(SPS_BWD_DQ | SPS_BWD_DKDV, family, B, H, N, D, dtype, q, q_strides, k, k_strides, v,
+                       v_strides, o, o_strides, dout, dout_strides, lse, dq, dq_strides, dk, dk_strides, dv,
+                       dv_strides, docs, docs_dtype, docs_stride_b, sm_scale, window, has_pkw, pkw, workspace,
+                       workspace_bytes, stream);
+}
+
+int sps_attn_bwd_pass(int pass, int family, int B, int H, int N, int D, int dtype, const void* q,
+                      const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                      const int64_t* v_strides, const void* o, const int64_t* o_strides, const void* dout,
+                      const int64_t* dout_strides, const float* lse, void* dq, const int64_t* dq_strides, void* dk,
+                      const int64_t* dk_strides, void* dv, const int64_t* dv_strides, const void* docs,
+                      int docs_dtype, int64_t docs_stride_b, float sm_scale, int window, int has_pkw, int pkw,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (pass != SPS_BWD_DQ && pass != SPS_BWD_DKDV) {
+    g_last_error.clear();
+    return fail(SPS_E_INVALID, "pass must be SPS_BWD_DQ or SPS_BWD_DKDV (got %d)", pass);
+  }
+  return attn_bwd_impl(pass, family, B, H, N, D, dtype, q, q_strides, k, k_strides, v, v_strides, o, o_strides,
+                       dout, dout_strides, lse, dq, dq_strides, dk, dk_strides, dv, dv_strides, docs, docs_dtype,
+                       docs_stride_b, sm_scale, window, has_pkw, pkw, workspace, workspace_bytes, stream);
 }
 
 int sps_attn_mask(int family, int B, int N, const void* docs, int docs_dtype, int64_t docs_stride_b, int window,

@@ -44,8 +44,13 @@ __device__ __forceinline__ void unpack16(const u32x4_t w, float* out) {
       out[2 * i + 1] = KV::cvt((uint16_t)(w[i] >> 16));
     }
   } else {
+    // Copy each element to a scalar first: clang lowers __builtin_bit_cast of a vector-element
+    // subscript (an lvalue) as a read of element 0.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = __builtin_bit_cast(float, w[i]);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t x = w[i];
+      out[i] = __builtin_bit_cast(float, x);
+    }
   }
 }
 
