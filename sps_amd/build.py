@@ -29,9 +29,13 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA results in VGPRs (gfx950's unified register file): without it the backend routes every
+    # accumulator through one AGPR tile with v_accvgpr copies around each MFMA.
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form=1",
 ]
 
-SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "decode.hip", "capi.cpp"]
+SOURCES = ["attn_prep.hip", "attn_fwd.hip", "attn_bwd.hip", "decode.hip", "capi.cpp"]
 
 
 def _hipcc() -> str:

@@ -2,61 +2,55 @@
 //
 // One workgroup = 4 waves = 128 query positions; each wave owns 32 queries. Per 32-key block the
 // wave computes S^T = K Q^T with v_mfma_f32_32x32x16 (K rows from LDS, Q held in registers), so
-// every lane owns one query column: the online-softmax state (running max, running sum, rescale
-// factor) is lane-local and the row reductions need a single permlane32 swap. O^T += V^T P^T
-// takes V^T fragments straight out of the row-major LDS tile with ds_read_b64_tr_b16 and P^T from
-// the score accumulator converted to 16-bit pairs in place. K/V tiles are double-buffered in LDS
-// with one barrier per block; the next block's global loads are in flight during the MFMAs.
+// every lane owns one query column: the online-softmax state is lane-local and row reductions need a
+// single permlane32 swap. O^T += V^T P^T takes V^T fragments straight out of the row-major LDS
+// tile with ds_read_b64_tr_b16 and P^T from the score accumulator converted to 16-bit pairs in
+// place.
+//
+// Schedule: the workgroup's key blocks are the union of its lanes' visible intervals (one range of
+// 32-row blocks per key stream, computed once from the prepass's run starts), and each wave
+// classifies each block from four numbers (attn_sched.hpp), so no per-block lookups go to memory.
+// K/V blocks flow global -> registers -> LDS through a ring of R register sets: a block's loads are
+// issued R blocks before it is computed, the LDS tiles are double-buffered, one barrier per block.
+//
+// Softmax: exp2 domain with log2(e) folded into the scale; the running max is only raised (and the
+// accumulator rescaled) when a block's max exceeds it by more than 2^8, so P stays <= 256 and most
+// blocks skip the rescale; row sums of P use v_dot2 on the packed 16-bit P the MFMA consumes.
 //
 // Reference semantics: _attn_fwd_sps / _attn_fwd_inner_sps (triton_sps_flash_attention.py:26-269),
 // _attn_fwd (triton_reverse_sps_flash_attention.py:242-331, triton_full_flash_attention.py:204-283):
-// exp2-domain online softmax with the scale folded into log2(e); P is rounded to the input type
-// before the PV product; LSE = m + log2(l) is saved for the backward pass.
+// P is rounded to the input type before the PV product; LSE = m + log2(l) is saved for the backward.
 #include "attn_tiles.hpp"
 
 namespace sps {
 
-__global__ void doc_granules_kernel(const AttnArgs a) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= a.B * a.NG) return;
-  const int b = idx / a.NG, gi = idx - b * a.NG;
-  const int lo = gi * kGranule;
-  const int hi = lo + kGranule < a.m.N ? lo + kGranule : a.m.N;
-  int64_t mn = INT64_MAX, mx = INT64_MIN;
-  for (int p = lo; p < hi; ++p) {
-    const int64_t d = load_doc(a, b, p);
-    mn = d < mn ? d : mn;
-    mx = d > mx ? d : mx;
-  }
-  a.gmin[idx] = mn;
-  a.gmax[idx] = mx;
-}
+constexpr float kRescaleThreshold = 8.0f;
 
-template <int D, class E>
+template <int D, class E, int R>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
+  static_assert(R % 2 == 0, "the register ring depth must be even (static LDS buffer indices)");
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][G::ELEMS];
   __shared__ __attribute__((aligned(16))) uint16_t sV[2][G::ELEMS];
-  __shared__ int64_t sDoc[2][kBlock];
+  __shared__ int s_span[4 * kWaves];
 
   const MaskSpec m = a.m;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c32 = lane & 31;
-
-  const int nqt = (m.N + kTile - 1) / kTile;
-  const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = lid / nqt;
-  const int qt = nqt - 1 - (lid - bh * nqt);  // later (heavier) query tiles first
-  const int b = bh / a.H, h = bh - b * a.H;
-  const int qa = qt * kTile;
-  const int qw = qa + wave * kBlock;
-  const int qp = qw + c32;
+  int b, h, qt;
+  q_workgroup(a, b, h, qt);
+  const RowView row = row_view(a, b);
+  const int qp = qt * kTile + wave * kBlock + c32;
   const bool qvalid = qp < m.N;
+  QState st;
+  q_setup(a, row, qp, s_span, st);
+  const QPlan& plan = st.plan;
+  const int nb = plan.count();
+  const bool exact = row.mono;
+  const int64_t dq_doc = (!exact && qvalid) ? load_doc(a, b, qp) : 0;
 
   const uint16_t* kbase = a.k + b * a.sk.b + h * a.sk.h;
   const uint16_t* vbase = a.v + b * a.sv.b + h * a.sv.h;
-  const int64_t* gmin = a.gmin + (int64_t)b * a.NG;
-  const int64_t* gmax = a.gmax + (int64_t)b * a.NG;
 
   // Q fragments: B operand of S^T = K Q^T (lane: query c32, d = 16c + 8g .. +7).
   u32x4_t qf[D / 16];
@@ -68,110 +62,113 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
       qf[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(qrow + 16 * c + 8 * g) : z;
     }
   }
-  const int64_t dq = (m.has_docs && qvalid) ? load_doc(a, b, qp) : 0;
-
-  const QSchedule s = make_qschedule(m, qa);
-  const int nb = s.n0 + s.n1;
-  const int wg_qhi = qa + kTile - 1 < m.N - 1 ? qa + kTile - 1 : m.N - 1;
-  const int w_qhi = qw + kBlock - 1 < m.N - 1 ? qw + kBlock - 1 : m.N - 1;
-  DocRange wg_qd = {0, 0}, w_qd = {0, 0};
-  if (m.has_docs) {
-    wg_qd = doc_range(gmin, gmax, qa, wg_qhi);
-    if (qw < m.N) w_qd = doc_range(gmin, gmax, qw, w_qhi);
-  }
 
   zero_pad_cols<D>(sK[0], tid);
   zero_pad_cols<D>(sK[1], tid);
   zero_pad_cols<D>(sV[0], tid);
   zero_pad_cols<D>(sV[1], tid);
 
-  TileRegs<D> rk, rv;
-  int64_t rdoc = 0;
-  auto load_block = [&](const KeyRun& kr) {
-    auto pos = [&](int r) { return key_pos(m, kr, r); };
-    rk.load(kbase, a.sk.n, m.N, tid, pos);
-    rv.load(vbase, a.sv.n, m.N, tid, pos);
-    if (m.has_docs && tid < kBlock) {
-      const int kp = pos(tid);
-      rdoc = kp < m.N ? load_doc(a, b, kp) : INT64_MIN;
-    }
+  TileRegs<D> rk[R], rv[R];
+  auto issue = [&](int i, TileRegs<D>& tk, TileRegs<D>& tv) {
+    const int s = plan.stream(i);
+    const int pos0 = stream_pos(m, s, plan.first(i));
+    const int step = s == STREAM_NATURAL ? 1 : 2;
+    tk.load(kbase, a.sk.n, m.N, tid, pos0, step);
+    tv.load(vbase, a.sv.n, m.N, tid, pos0, step);
   };
-  auto store_block = [&](int buf) {
-    rk.store(sK[buf], tid);
-    rv.store(sV[buf], tid);
-    if (m.has_docs && tid < kBlock) sDoc[buf][tid] = rdoc;
-  };
+
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    if (j < nb) issue(j, rk[j], rv[j]);
+  if (nb > 0) {
+    rk[0].store(sK[0], tid);
+    rv[0].store(sV[0], tid);
+  }
+  if (R < nb) issue(R, rk[0], rv[0]);
+  __syncthreads();
 
   float m_run = -INFINITY, l_run = 0.f;
   f32x16_t acc[G::DC];
 #pragma unroll
   for (int dc = 0; dc < G::DC; ++dc) acc[dc] = f32x16_t{};
 
-  int cur = qs_next_block(m, s, qa, wg_qhi, wg_qd, gmin, gmax, -1);
-  KeyRun kr_cur = qschedule_block(s, cur < nb ? cur : 0);
-  if (cur < nb) {
-    load_block(kr_cur);
-    store_block(0);
-  }
-  __syncthreads();
-  int buf = 0;
-  while (cur < nb) {
-    const int nxt = qs_next_block(m, s, qa, wg_qhi, wg_qd, gmin, gmax, cur);
-    const KeyRun kr_nxt = qschedule_block(s, nxt < nb ? nxt : 0);
-    if (nxt < nb) load_block(kr_nxt);
+  vmem_wait_all();
+  // Two copies of the loop: exact interval masks (ids non-decreasing), or interval + id checks.
+  auto run = [&](auto exact_tag) {
+    constexpr bool EXACT = decltype(exact_tag)::value;
+    for (int i0 = 0; i0 < nb; i0 += R) {
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        const int i = i0 + u;
+        if (i < nb) {
+          const int nslot = (u + 1) % R;
+          if (i + 1 < nb) {
+            rk[nslot].store(sK[(u + 1) & 1], tid);
+            rv[nslot].store(sV[(u + 1) & 1], tid);
+          }
+          if (i + 1 + R < nb) issue(i + 1 + R, rk[nslot], rv[nslot]);
 
-    const int cls = classify(m, qw, w_qhi, kr_cur, w_qd, run_docs(m, kr_cur, gmin, gmax));
-    if (cls != TILE_SKIP) {
-      const uint16_t* tK = sK[buf];
-      const uint16_t* tV = sV[buf];
-      f32x16_t sc = {};
+          const bool s0 = i < plan.n0;
+          const int t0 = plan.first(i);
+          const WaveSpan ws = s0 ? st.w0 : st.w1;
+          const Interval lr = s0 ? st.r0 : st.r1;
+          const int cls = classify_block(ws, t0, EXACT);
+          if (cls != TILE_SKIP) {
+            const uint16_t* tK = sK[u & 1];
+            const uint16_t* tV = sV[u & 1];
+            f32x16_t sc = {};
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c)
-        sc = E::mfma(lds_read_b128(tK + c32 * G::RS + 16 * c + 8 * g), qf[c], sc);
-      if (cls == TILE_PARTIAL) {
-        const uint32_t bits = qs_mask_bits(m, qp, dq, kr_cur, g, sDoc[buf]);
+            for (int c = 0; c < D / 16; ++c)
+              sc = E::mfma(lds_read_b128(tK + c32 * G::RS + 16 * c + 8 * g), qf[c], sc);
+            if (cls == TILE_PARTIAL) {
+              if constexpr (EXACT) {
+                mask_outside(sc, lr.lo, lr.hi, t0, g);
+              } else {
+                const uint32_t bits = qs_exact_bits(a, b, lr, plan.stream(i), t0, g, dq_doc);
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (!((bits >> i) & 1u)) sc[i] = -INFINITY;
-      }
-      float mx = sc[0];
+                for (int e = 0; e < 16; ++e) sc[e] = ((bits >> e) & 1u) ? sc[e] : -INFINITY;
+              }
+            }
+            float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
 #pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sc[i]);
-      mx = half_max(mx);
-      const float m_new = fmaxf(m_run, mx * a.scale2);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      float rs = 0.f;
-      uint32_t pk[8];
+            for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, sc[e]), sc[e + 1]);
+            mx = fmaxf(mx, sc[15]);
+            const float mb = half_max(mx) * a.scale2;
+            const bool need = mb > m_run + kRescaleThreshold;
+            if (wave_any(need)) {
+              const float alpha = need ? fast_exp2(m_run - mb) : 1.f;
+              m_run = need ? mb : m_run;
+              l_run *= alpha;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float p0 = fast_exp2(fmaf(sc[2 * j], a.scale2, -m_use));
-        const float p1 = fast_exp2(fmaf(sc[2 * j + 1], a.scale2, -m_use));
-        rs += p0 + p1;
-        pk[j] = E::pack2(p0, p1);
-      }
-      l_run = fmaf(l_run, alpha, rs);
-      m_run = m_new;
-      if (wave_any(alpha != 1.f)) {
+              for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
+            }
+            const float mu = m_run == -INFINITY ? 0.f : m_run;
+            uint32_t pk[8];
 #pragma unroll
-        for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
-      }
+            for (int j = 0; j < 8; ++j) {
+              const float p0 = fast_exp2(fmaf(sc[2 * j], a.scale2, -mu));
+              const float p1 = fast_exp2(fmaf(sc[2 * j + 1], a.scale2, -mu));
+              pk[j] = E::pack2(p0, p1);
+              l_run = E::sum2(pk[j], l_run);
+            }
 #pragma unroll
-      for (int dc = 0; dc < G::DC; ++dc) {
+            for (int dc = 0; dc < G::DC; ++dc) {
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          const u32x4_t pf = {pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]};
-          acc[dc] = E::mfma(lds_frag_tr(tV, G::RS, 16 * kh, 32 * dc, lane), pf, acc[dc]);
+              for (int kh = 0; kh < 2; ++kh) {
+                const u32x4_t pf = {pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]};
+                acc[dc] = E::mfma(lds_frag_tr(tV, G::RS, 16 * kh, 32 * dc, lane), pf, acc[dc]);
+              }
+            }
+          }
+          __syncthreads();
         }
       }
     }
-
-    if (nxt < nb) store_block(buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
-    cur = nxt;
-    kr_cur = kr_nxt;
-  }
+  };
+  if (exact)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
 
   // Epilogue: combine the two halves' partial sums, normalise, store O (lane = query row) and LSE.
   const float l_tot = half_sum(l_run);
@@ -190,69 +187,49 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
         }
       }
     }
-    if (g == 0) a.lse[(int64_t)bh * m.N + qp] = l_tot > 0.f ? m_run + __log2f(l_tot) : -INFINITY;
+    if (g == 0) a.lse[((int64_t)b * a.H + h) * m.N + qp] = l_tot > 0.f ? m_run + __log2f(l_tot) : -INFINITY;
   }
 }
 
 // Writes the visibility mask exactly as the query-stationary kernels (forward, dQ) evaluate it:
-// same block schedule, same per-wave classification, same per-element predicate and lane layout.
+// same plan, same per-wave classification, same per-element tests and lane layout.
 __global__ __launch_bounds__(256) void mask_dump_q_kernel(const AttnArgs a) {
-  __shared__ int64_t sDoc[kBlock];
+  __shared__ int s_span[4 * kWaves];
   const MaskSpec m = a.m;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c32 = lane & 31;
-  const int nqt = (m.N + kTile - 1) / kTile;
-  const int b = blockIdx.x / nqt;
-  const int qa = (blockIdx.x - b * nqt) * kTile;
-  const int qw = qa + wave * kBlock;
-  const int qp = qw + c32;
+  int b, h, qt;
+  q_workgroup(a, b, h, qt);
+  const RowView row = row_view(a, b);
+  const int qp = qt * kTile + wave * kBlock + c32;
   const bool qvalid = qp < m.N;
-  const int64_t* gmin = a.gmin + (int64_t)b * a.NG;
-  const int64_t* gmax = a.gmax + (int64_t)b * a.NG;
-  const int64_t dq = (m.has_docs && qvalid) ? load_doc(a, b, qp) : 0;
-  const QSchedule s = make_qschedule(m, qa);
-  const int nb = s.n0 + s.n1;
-  const int wg_qhi = qa + kTile - 1 < m.N - 1 ? qa + kTile - 1 : m.N - 1;
-  const int w_qhi = qw + kBlock - 1 < m.N - 1 ? qw + kBlock - 1 : m.N - 1;
-  DocRange wg_qd = {0, 0}, w_qd = {0, 0};
-  if (m.has_docs) {
-    wg_qd = doc_range(gmin, gmax, qa, wg_qhi);
-    if (qw < m.N) w_qd = doc_range(gmin, gmax, qw, w_qhi);
-  }
-  uint8_t* mrow = a.mask_out + ((int64_t)b * m.N + qp) * m.N;
-  for (int cur = qs_next_block(m, s, qa, wg_qhi, wg_qd, gmin, gmax, -1); cur < nb;
-       cur = qs_next_block(m, s, qa, wg_qhi, wg_qd, gmin, gmax, cur)) {
-    const KeyRun kr = qschedule_block(s, cur);
-    if (m.has_docs && tid < kBlock) {
-      const int kp = key_pos(m, kr, tid);
-      sDoc[tid] = kp < m.N ? load_doc(a, b, kp) : INT64_MIN;
+  QState st;
+  q_setup(a, row, qp, s_span, st);
+  const QPlan& plan = st.plan;
+  const bool exact = row.mono;
+  const int64_t dq_doc = (!exact && qvalid) ? load_doc(a, b, qp) : 0;
+  uint8_t* mrow = a.mask_out + ((int64_t)b * m.N + (qvalid ? qp : 0)) * m.N;
+  for (int i = 0; i < plan.count(); ++i) {
+    const bool s0 = i < plan.n0;
+    const int t0 = plan.first(i), stream = plan.stream(i);
+    const WaveSpan ws = s0 ? st.w0 : st.w1;
+    const Interval lr = s0 ? st.r0 : st.r1;
+    const int cls = classify_block(ws, t0, exact);
+    if (cls == TILE_SKIP || !qvalid) continue;
+    uint32_t bits = 0xffffu;
+    if (cls == TILE_PARTIAL)
+      bits = exact ? interval_keep_bits(lr.lo, lr.hi, t0, g) : qs_exact_bits(a, b, lr, stream, t0, g, dq_doc);
+    for (int e = 0; e < 16; ++e) {
+      if ((bits >> e) & 1u) mrow[stream_pos(m, stream, t0 + acc_row(e, g))] = 1;
     }
-    __syncthreads();
-    const int cls = classify(m, qw, w_qhi, kr, w_qd, run_docs(m, kr, gmin, gmax));
-    if (cls != TILE_SKIP && qvalid) {
-      const uint32_t bits = cls == TILE_FULL ? 0xffffu : qs_mask_bits(m, qp, dq, kr, g, sDoc);
-      for (int i = 0; i < 16; ++i) {
-        const int kp = key_pos(m, kr, acc_row(i, g));
-        if ((bits >> i) & 1u) mrow[kp] = 1;
-      }
-    }
-    __syncthreads();
   }
-}
-
-hipError_t launch_doc_granules(const AttnArgs& a, hipStream_t stream) {
-  const int n = a.B * a.NG;
-  if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(doc_granules_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, a);
-  return hipGetLastError();
 }
 
 template <int D, class E>
 static hipError_t launch_fwd_t(const AttnArgs& a, hipStream_t stream) {
-  const int nqt = (a.m.N + kTile - 1) / kTile;
-  const int64_t nblocks = (int64_t)nqt * a.B * a.H;
+  const int64_t nblocks = (int64_t)q_tiles(a.m.N) * a.B * a.H;
   if (nblocks == 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3((unsigned)nblocks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, E, 2>), dim3((unsigned)nblocks), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -272,8 +249,7 @@ hipError_t launch_attn_fwd(const AttnArgs& a, int D, int is_f16, hipStream_t str
 }
 
 hipError_t launch_mask_dump_q(const AttnArgs& a, hipStream_t stream) {
-  const int nqt = (a.m.N + kTile - 1) / kTile;
-  const int n = nqt * a.B;
+  const int n = q_tiles(a.m.N) * a.B * a.H;
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(mask_dump_q_kernel, dim3(n), dim3(256), 0, stream, a);
   return hipGetLastError();

@@ -18,19 +18,22 @@ struct AttnArgs {
   const uint16_t* v;
   const uint16_t* o;
   const uint16_t* dO;
-  uint16_t* out;  // forward: O; unused by the backward kernels
+  uint16_t* out;  // forward: O
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
   Strides3 sq, sk, sv, so, sdo, sout, sdq, sdk, sdv;
-  float* lse;          // [B, H, N] log2-domain log-sum-exp of the scaled scores
-  float* delta;        // [B, H, N] rowsum(O * dO) (backward)
-  const void* docs;    // [B, N] int32 or int64 document ids (unit stride along N), or null
+  float* lse;        // [B, H, N] log2-domain log-sum-exp of the scaled scores
+  float* delta;      // [B, H, N] rowsum(O * dO) (backward)
+  const void* docs;  // [B, N] int32 or int64 document ids (unit stride along N), or null
   int docs_i64;
   int64_t docs_sb;
-  int64_t* gmin;  // [B, NG] per-granule min/max document id (written by the prepass)
-  int64_t* gmax;
-  int NG;
+  // Row layout written by the prepass when docs are given (workspace), else null:
+  int* run_start;  // [B, N] first position of the run of equal ids containing each position
+  int* run_end;    // [B, N] last position of that run
+  int* row_mono;   // [B] 1 when the row's ids are non-decreasing (runs are the documents)
+  int* q_order;    // [B, q_tiles] query tiles, heaviest first
+  int* k_order;    // [B, k_tiles] key tiles, heaviest first
   int B, H;
   float sm_scale;
   float scale2;  // sm_scale * log2(e)
@@ -43,13 +46,50 @@ __device__ __forceinline__ int64_t load_doc(const AttnArgs& a, int b, int pos) {
   return reinterpret_cast<const int32_t*>(a.docs)[b * a.docs_sb + pos];
 }
 
-// Host launchers (each defined next to its kernels). All launches are asynchronous on `stream`.
-hipError_t launch_doc_granules(const AttnArgs& a, hipStream_t stream);
-hipError_t launch_attn_fwd(const AttnArgs& a, int D, int is_f16, hipStream_t stream);
+// Row view used by the kernels: run bounds of a position and whether ids need an exact check.
+struct RowView {
+  const int* start;  // null: no documents (one run covering the row)
+  const int* end;
+  bool mono;
+  __device__ __forceinline__ int run_start(int p) const { return start ? start[p] : 0; }
+  __device__ __forceinline__ int run_end(int p, int N) const { return end ? end[p] : N - 1; }
+};
+
+__device__ __forceinline__ RowView row_view(const AttnArgs& a, int b) {
+  RowView r;
+  if (a.m.has_docs) {
+    r.start = a.run_start + (int64_t)b * a.m.N;
+    r.end = a.run_end + (int64_t)b * a.m.N;
+    r.mono = a.row_mono[b] != 0;
+  } else {
+    r.start = nullptr;
+    r.end = nullptr;
+    r.mono = true;
+  }
+  return r;
+}
+
+// Query tile processed by workgroup rank `rank` of row b (heaviest first).
+__device__ __forceinline__ int q_tile_of(const AttnArgs& a, int b, int rank) {
+  const int nqt = q_tiles(a.m.N);
+  if (a.m.has_docs) return a.q_order[b * nqt + rank];
+  return nqt - 1 - rank;
+}
+
+__device__ __forceinline__ int k_tile_of(const AttnArgs& a, int b, int rank) {
+  const int nkt = k_tiles(a.m.family, a.m.N, a.m.P);
+  if (a.m.has_docs) return a.k_order[b * nkt + rank];
+  return rank;
+}
+
 // Backward passes (bit mask): kBwdDq computes Delta = rowsum(O * dO) and dQ; kBwdDkdv computes dK and dV
 // from the Delta the dQ pass stored.
 constexpr int kBwdDq = 1;
 constexpr int kBwdDkdv = 2;
+
+// Host launchers (each defined next to its kernels). All launches are asynchronous on `stream`.
+hipError_t launch_row_layout(const AttnArgs& a, hipStream_t stream);
+hipError_t launch_attn_fwd(const AttnArgs& a, int D, int is_f16, hipStream_t stream);
 hipError_t launch_attn_bwd(const AttnArgs& a, int D, int is_f16, int passes, hipStream_t stream);
 hipError_t launch_mask_dump(const AttnArgs& a, int schedule, hipStream_t stream);
 

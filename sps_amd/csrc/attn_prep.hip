@@ -1,0 +1,182 @@
+// Row-layout prepass of the attention kernels (one workgroup per batch row).
+//
+// From a row's document ids it writes, for every position, the first and last position of the
+// maximal run of equal ids containing it, and whether the row's ids are non-decreasing. In a
+// non-decreasing row every document is one run, so the attention kernels turn the document mask
+// into interval bounds (see attn_sched.hpp). A row with decreasing steps is recorded as one run
+// covering the row (start 0, end N - 1) and the kernels compare ids pair by pair there.
+//
+// It also writes the row's query tiles and key tiles in decreasing order of their (approximate)
+// number of MFMA blocks, so the heaviest workgroups are dispatched first. The order only affects
+// speed: it is always a permutation of the tiles.
+#include "attn_kernels.hpp"
+
+namespace sps {
+
+constexpr int kPrepThreads = 1024;
+constexpr int kRegIds = 8;  // ids per thread held in registers (rows up to kPrepThreads * kRegIds positions)
+constexpr int kMaxSortTiles = 2048;  // rows with more tiles keep the closed-form order
+
+__device__ __forceinline__ int blocks_in(int lo, int hi) {
+  return hi >= lo ? (hi >> 5) - (lo >> 5) + 1 : 0;
+}
+
+// Key blocks of the query tile qt (both streams), from its first and last queries' intervals.
+__device__ int q_tile_cost(const MaskSpec& m, const int* start, int qt) {
+  const int qa = qt * kTile, qz = imin(qa + kTile - 1, m.N - 1);
+  Interval a0, a1, z0, z1;
+  query_intervals(m, qa, start[qa], a0, a1);
+  query_intervals(m, qz, start[qz], z0, z1);
+  return blocks_in(imin(a0.lo, z0.lo), imax(a0.hi, z0.hi)) + blocks_in(imin(a1.lo, z1.lo), imax(a1.hi, z1.hi));
+}
+
+// Query chunks of the key tile kt, from its first key and the last query of its last key.
+__device__ int k_tile_cost(const MaskSpec& m, const int* end, int kt) {
+  int stream, first;
+  k_tile_run(m, kt, stream, first);
+  const int len = stream_len(m.family, m.N, stream, m.P);
+  const int last = imin(first + kTile - 1, len - 1);
+  const int k0 = stream_pos(m, stream, first), k1 = stream_pos(m, stream, last);
+  return blocks_in(k0, key_last_query(m, stream, k1, end[k1]));
+}
+
+// Exclusive scans over the per-thread chunk summaries (Hillis-Steele in LDS).
+template <class Op>
+__device__ int block_exclusive_scan(int* s, int x, int identity, Op op, bool reverse) {
+  const int tid = threadIdx.x;
+  const int slot = reverse ? kPrepThreads - 1 - tid : tid;
+  s[slot] = x;
+  __syncthreads();
+  for (int o = 1; o < kPrepThreads; o <<= 1) {
+    const int y = slot >= o ? s[slot - o] : identity;
+    __syncthreads();
+    s[slot] = op(s[slot], y);
+    __syncthreads();
+  }
+  const int r = slot > 0 ? s[slot - 1] : identity;
+  __syncthreads();
+  return r;
+}
+
+// Writes the order of `n` tiles by decreasing cost (ties: lower index first) into order[0..n).
+__device__ void sort_tiles(const int* cost, int n, int* order, bool ascending_fallback) {
+  const int tid = threadIdx.x;
+  if (n > kMaxSortTiles) {
+    for (int t = tid; t < n; t += kPrepThreads) order[t] = ascending_fallback ? t : n - 1 - t;
+    return;
+  }
+  for (int t = tid; t < n; t += kPrepThreads) {
+    const int c = cost[t];
+    int r = 0;
+    for (int j = 0; j < n; ++j) r += (cost[j] > c) || (cost[j] == c && j < t);
+    order[r] = t;
+  }
+}
+
+__global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs a) {
+  __shared__ int s_scan[kPrepThreads];
+  __shared__ int s_cost[kMaxSortTiles];
+  __shared__ int s_nonmono;
+  const MaskSpec m = a.m;
+  const int b = blockIdx.x, tid = threadIdx.x, N = m.N;
+  int* start = a.run_start + (int64_t)b * N;
+  int* end = a.run_end + (int64_t)b * N;
+  const int C = (N + kPrepThreads - 1) / kPrepThreads;
+  const int p0 = imin(tid * C, N), p1 = imin(p0 + C, N);
+  if (tid == 0) s_nonmono = 0;
+
+  const bool in_regs = C <= kRegIds;
+  int last = -1, first = N;
+  bool dec = false;
+  int64_t d[kRegIds];
+  bool flag[kRegIds];
+  if (in_regs) {
+    // Common case: every id of this thread's chunk (and its predecessor) loaded once, together.
+    const int64_t before = (p0 > 0 && p0 < N) ? load_doc(a, b, p0 - 1) : 0;
+#pragma unroll
+    for (int j = 0; j < kRegIds; ++j) d[j] = p0 + j < p1 ? load_doc(a, b, p0 + j) : 0;
+#pragma unroll
+    for (int j = 0; j < kRegIds; ++j) {
+      const int p = p0 + j;
+      const int64_t prev = j == 0 ? before : d[j - 1];
+      flag[j] = p < p1 && (p == 0 || d[j] != prev);
+      dec |= p < p1 && p > 0 && d[j] < prev;
+      if (flag[j]) {
+        last = p;
+        first = imin(first, p);
+      }
+    }
+  } else {
+    int64_t prev = p0 > 0 ? load_doc(a, b, p0 - 1) : 0;
+    for (int p = p0; p < p1; ++p) {
+      const int64_t x = load_doc(a, b, p);
+      if (p == 0 || x != prev) {
+        last = p;
+        first = imin(first, p);
+      }
+      dec |= (p > 0 && x < prev);
+      prev = x;
+    }
+  }
+  __syncthreads();
+  if (dec) atomicOr(&s_nonmono, 1);
+  const int carry_start = block_exclusive_scan(s_scan, last, -1, [](int x, int y) { return imax(x, y); }, false);
+  const int carry_next = block_exclusive_scan(s_scan, first, N, [](int x, int y) { return imin(x, y); }, true);
+  const bool mono = s_nonmono == 0;
+
+  if (mono && in_regs) {
+    int cur = carry_start;
+#pragma unroll
+    for (int j = 0; j < kRegIds; ++j) {
+      if (flag[j]) cur = p0 + j;
+      if (p0 + j < p1) start[p0 + j] = cur;
+    }
+    int nxt = carry_next;
+#pragma unroll
+    for (int j = kRegIds - 1; j >= 0; --j) {
+      if (p0 + j < p1) end[p0 + j] = nxt - 1;
+      if (flag[j]) nxt = p0 + j;
+    }
+  } else if (mono) {
+    int cur = carry_start;
+    int64_t prev = p0 > 0 ? load_doc(a, b, p0 - 1) : 0;
+    for (int p = p0; p < p1; ++p) {
+      const int64_t x = load_doc(a, b, p);
+      if (p == 0 || x != prev) cur = p;
+      start[p] = cur;
+      prev = x;
+    }
+    int nxt = carry_next;
+    for (int p = p1 - 1; p >= p0; --p) {
+      end[p] = nxt - 1;
+      if (p == 0 || load_doc(a, b, p) != load_doc(a, b, p - 1)) nxt = p;
+    }
+  } else {
+    for (int p = p0; p < p1; ++p) {
+      start[p] = 0;
+      end[p] = N - 1;
+    }
+  }
+  if (tid == 0) a.row_mono[b] = mono ? 1 : 0;
+  __syncthreads();  // start/end of the whole row are visible to every thread below
+
+  const int nqt = q_tiles(N);
+  if (nqt <= kMaxSortTiles)
+    for (int t = tid; t < nqt; t += kPrepThreads) s_cost[t] = q_tile_cost(m, start, t);
+  __syncthreads();
+  sort_tiles(s_cost, nqt, a.q_order + (int64_t)b * nqt, false);
+  __syncthreads();
+  const int nkt = k_tiles(m.family, N, m.P);
+  if (nkt <= kMaxSortTiles)
+    for (int t = tid; t < nkt; t += kPrepThreads) s_cost[t] = k_tile_cost(m, end, t);
+  __syncthreads();
+  sort_tiles(s_cost, nkt, a.k_order + (int64_t)b * nkt, true);
+}
+
+hipError_t launch_row_layout(const AttnArgs& a, hipStream_t stream) {
+  if (a.B == 0 || a.m.N == 0 || !a.m.has_docs) return hipSuccess;
+  hipLaunchKernelGGL(row_layout_kernel, dim3(a.B), dim3(kPrepThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace sps

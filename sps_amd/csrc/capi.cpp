@@ -56,24 +56,26 @@ sps::Strides3 strides(const int64_t* st) {
 bool supported_head_dim(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
 struct AttnLayout {
-  size_t gmin, gmax, delta, total;
+  size_t run_start, run_end, row_mono, q_order, k_order, delta, total;
 };
 
 AttnLayout attn_layout(int family, int B, int H, int N, int has_docs, int backward) {
-  (void)family;
-  AttnLayout l = {0, 0, 0, 0};
-  const size_t NG = (size_t)(N + sps::kGranule - 1) / sps::kGranule;
+  AttnLayout l = {0, 0, 0, 0, 0, 0, 0};
   size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off = align_up(off + bytes);
+    return at;
+  };
   if (has_docs) {
-    l.gmin = off;
-    off = align_up(off + (size_t)B * NG * sizeof(int64_t));
-    l.gmax = off;
-    off = align_up(off + (size_t)B * NG * sizeof(int64_t));
+    const int P = family == SPS_FAMILY_REVERSE_SPS ? 1 : 0;
+    l.run_start = take((size_t)B * N * sizeof(int));
+    l.run_end = take((size_t)B * N * sizeof(int));
+    l.row_mono = take((size_t)B * sizeof(int));
+    l.q_order = take((size_t)B * sps::q_tiles(N) * sizeof(int));
+    l.k_order = take((size_t)B * sps::k_tiles(family, N, P) * sizeof(int));
   }
-  if (backward) {
-    l.delta = off;
-    off = align_up(off + (size_t)B * H * N * sizeof(float));
-  }
+  if (backward) l.delta = take((size_t)B * H * N * sizeof(float));
   l.total = off;
   return l;
 }
@@ -87,6 +89,7 @@ int setup_common(sps::AttnArgs& a, int family, int B, int H, int N, const void* 
   if (B < 0 || H < 0 || N < 0) return fail(SPS_E_INVALID, "negative size B=%d H=%d N=%d", B, H, N);
   if (family != SPS_FAMILY_FULL && (N % 2) != 0)
     return fail(SPS_E_INVALID, "SPS families need an even sequence length (2T), got N=%d", N);
+  if (N > (1 << 28)) return fail(SPS_E_UNSUPPORTED, "sequence length %d too large", N);
   if (docs && docs_dtype != SPS_DTYPE_I32 && docs_dtype != SPS_DTYPE_I64)
     return fail(SPS_E_INVALID, "document ids must be int32 or int64 (dtype code %d)", docs_dtype);
   const AttnLayout l = attn_layout(family, B, H, N, docs != nullptr, backward);
@@ -98,18 +101,24 @@ int setup_common(sps::AttnArgs& a, int family, int B, int H, int N, const void* 
   a.docs = docs;
   a.docs_i64 = docs_dtype == SPS_DTYPE_I64;
   a.docs_sb = docs_stride_b;
-  a.NG = (N + sps::kGranule - 1) / sps::kGranule;
-  a.gmin = docs ? reinterpret_cast<int64_t*>(ws + l.gmin) : nullptr;
-  a.gmax = docs ? reinterpret_cast<int64_t*>(ws + l.gmax) : nullptr;
+  if (docs) {
+    a.run_start = reinterpret_cast<int*>(ws + l.run_start);
+    a.run_end = reinterpret_cast<int*>(ws + l.run_end);
+    a.row_mono = reinterpret_cast<int*>(ws + l.row_mono);
+    a.q_order = reinterpret_cast<int*>(ws + l.q_order);
+    a.k_order = reinterpret_cast<int*>(ws + l.k_order);
+  }
   a.delta = backward ? reinterpret_cast<float*>(ws + l.delta) : nullptr;
   a.B = B;
   a.H = H;
   a.m.family = family;
   a.m.P = family == SPS_FAMILY_REVERSE_SPS ? 1 : 0;
   a.m.N = N;
-  a.m.window = window;
+  // Distances never exceed N, so windows are clamped to [-1, N] (any negative window admits nothing
+  // but the persistent diagonal); this keeps the interval arithmetic inside int range.
+  a.m.window = window < -1 ? -1 : (window > N ? N : window);
   a.m.has_pkw = has_pkw ? 1 : 0;
-  a.m.pkw = pkw;
+  a.m.pkw = pkw < -1 ? -1 : (pkw > N ? N : pkw);
   a.m.has_docs = docs != nullptr;
   return SPS_OK;
 }
@@ -171,7 +180,7 @@ int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype, const void* 
   a.sm_scale = sm_scale;
   a.scale2 = sm_scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (docs && (rc = hip_status(sps::launch_doc_granules(a, s), "document prepass"))) return rc;
+  if (docs && (rc = hip_status(sps::launch_row_layout(a, s), "document prepass"))) return rc;
   return hip_status(sps::launch_attn_fwd(a, D, dtype == SPS_DTYPE_F16, s), "attention forward");
 }
 
@@ -221,8 +230,8 @@ static int attn_bwd_impl(int passes, int family, int B, int H, int N, int D, int
   a.sm_scale = sm_scale;
   a.scale2 = sm_scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // The document ranges are computed by the dQ pass and left in the workspace for the dK/dV pass.
-  if (docs && (passes & SPS_BWD_DQ) && (rc = hip_status(sps::launch_doc_granules(a, s), "document prepass")))
+  // The row layout is computed by the dQ pass and left in the workspace for the dK/dV pass.
+  if (docs && (passes & SPS_BWD_DQ) && (rc = hip_status(sps::launch_row_layout(a, s), "document prepass")))
     return rc;
   return hip_status(sps::launch_attn_bwd(a, D, dtype == SPS_DTYPE_F16, passes, s), "attention backward");
 }
@@ -273,7 +282,7 @@ int sps_attn_mask(int family, int B, int N, const void* docs, int docs_dtype, in
   if (!mask) return fail(SPS_E_INVALID, "mask: null pointer");
   a.mask_out = mask;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (docs && (rc = hip_status(sps::launch_doc_granules(a, s), "document prepass"))) return rc;
+  if (docs && (rc = hip_status(sps::launch_row_layout(a, s), "document prepass"))) return rc;
   return hip_status(sps::launch_mask_dump(a, schedule, s), "mask dump");
 }
 

@@ -48,6 +48,12 @@ struct ElemBF16 {
   static __device__ __forceinline__ float to_f32(uint16_t x) {
     return __builtin_bit_cast(float, (uint32_t)x << 16);
   }
+  // acc + lo + hi of a packed pair (v_dot2_f32_bf16 against {1, 1}).
+  static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
+    const uint32_t ones = 0x3f803f80u;
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair), __builtin_bit_cast(bf16x2_t, ones),
+                                          acc, false);
+  }
 };
 
 struct ElemF16 {
@@ -61,6 +67,11 @@ struct ElemF16 {
   }
   static __device__ __forceinline__ float to_f32(uint16_t x) {
     return (float)__builtin_bit_cast(_Float16, x);
+  }
+  // acc + lo + hi of a packed pair (v_dot2_f32_f16 against {1, 1}).
+  static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
+    const uint32_t ones = 0x3c003c00u;
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), __builtin_bit_cast(f16x2_t, ones), acc, false);
   }
 };
 
@@ -120,6 +131,11 @@ __device__ __forceinline__ float half_sum(float x) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
+// s_waitcnt vmcnt(0): waits for every outstanding vector-memory load of the wave. Placed before a
+// software-pipelined loop so the compiler's wait counting does not fall back to vmcnt(0) inside it
+// for registers loaded before the loop.
+__device__ __forceinline__ void vmem_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Reads a value that is uniform across the wave into a scalar register.
 __device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }

@@ -128,6 +128,9 @@ MASK_CASES = [
     ("full", 333, 0, "packed", None),
     ("full", 256, 0, "random", None),
     ("sps", 1024, 4096, "packed", None),
+    # rows longer than 8192 positions take the prepass's looped (not register-resident) path
+    ("sps", 8320, 64, "packed", None),
+    ("full", 8200, 0, "random", None),
 ]
 
 
@@ -152,11 +155,11 @@ def test_mask_bit_exact(case, schedule):
     assert (got == want).all(), f"{int((got != want).sum())} mismatching pairs"
 
 
-@pytest.mark.parametrize("family", ["sps", "full"])
-def test_visible_count_through_forward_kernel(family):
+@pytest.mark.parametrize("family,n", [("sps", 4096), ("full", 4096), ("reverse_sps", 8320)])
+def test_visible_count_through_forward_kernel(family, n):
     # Q = K = 0 makes every visible score equal, so the forward kernel's LSE is log2(#visible keys):
-    # an end-to-end check of the mask the real kernel applies, row by row, at a C3-like length.
-    n, b, h, d = 4096, 2, 2, 64
+    # an end-to-end check of the mask the real kernel applies, row by row, at C3-like lengths.
+    b, h, d = 2, 2, 64
     rng = np.random.default_rng(5)
     tokens = n if family == "full" else n // 2
     docs = _packed_docs(rng, b, tokens, family, max_len=900)
