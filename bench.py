@@ -72,11 +72,12 @@ def bench_attention(cfg, steps: int, warmup: int):
         e = [torch.cuda.Event(enable_timing=True) for _ in range(4)] if record else None
         if record:
             e[0].record()
-        o, lse, *_ = SA.attention_forward(q, k, v, scale, family, cfg.window, docs)
+        # The training step's path: the forward keeps its document layout for the backward.
+        o, lse, _, _, _, ws = SA.attention_forward(q, k, v, scale, family, cfg.window, docs, keep_layout=True)
         if record:
             e[1].record()
         SA.attention_backward(do, q, k, v, o, lse, scale, family, cfg.window, docs,
-                              between_passes=(e[2].record if record else None))
+                              between_passes=(e[2].record if record else None), layout_workspace=ws)
         if record:
             e[3].record()
             ev.append(e)

@@ -111,12 +111,18 @@ int sps_attn_bwd(int family, int B, int H, int N, int D, int dtype,
 #define SPS_BWD_DKDV 2 /* dk, dv from the Delta and document ranges the SPS_BWD_DQ pass left in the workspace
                           (reference: _sps_bwd_dkdv_kernel, triton_sps_flash_attention.py:272-382) */
 
+#define SPS_BWD_REUSE_LAYOUT 4 /* with SPS_BWD_DQ: the workspace already holds the document row layout
+                                  that sps_attn_fwd wrote for the same docs, family, N, window and pkw
+                                  (the forward was given a workspace of the backward's size), so the
+                                  pass skips recomputing it */
+
 /*
- * One pass of sps_attn_bwd, same arguments plus `pass` (SPS_BWD_DQ or SPS_BWD_DKDV). The SPS_BWD_DKDV
- * pass must follow an SPS_BWD_DQ pass with the same workspace on the same stream; arguments the pass
- * does not touch (dk, dv for SPS_BWD_DQ; dq for SPS_BWD_DKDV) are still validated. Lets a caller time
- * or schedule the two kernels separately, as the reference launches them separately
- * (triton_sps_flash_attention.py:651-707).
+ * Passes of sps_attn_bwd, same arguments plus `pass`: SPS_BWD_DQ, SPS_BWD_DKDV or both, optionally
+ * with SPS_BWD_REUSE_LAYOUT. An SPS_BWD_DKDV pass alone must follow an SPS_BWD_DQ pass with the same
+ * workspace on the same stream; arguments a pass does not touch (dk, dv for SPS_BWD_DQ; dq for
+ * SPS_BWD_DKDV) are still validated. Lets a caller time or schedule the two kernels separately, as the
+ * reference launches them separately (triton_sps_flash_attention.py:651-707), and reuse the forward's
+ * document layout.
  */
 int sps_attn_bwd_pass(int pass, int family, int B, int H, int N, int D, int dtype,
                       const void* q, const int64_t* q_strides,

@@ -25,6 +25,7 @@ DTYPE_I64 = 4
 
 BWD_DQ = 1
 BWD_DKDV = 2
+BWD_REUSE_LAYOUT = 4
 
 FAMILY_FULL = 0
 FAMILY_SPS = 1

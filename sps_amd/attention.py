@@ -95,14 +95,20 @@ def _validate(q, k, v, family, documents_idx_BxT):
         raise TypeError("q, k and v must share one dtype")
 
 
-def attention_forward(q, k, v, sm_scale, family, window=0, documents_idx_BxT=None, persistent_key_window=None):
-    """Runs the forward kernel; returns (o, lse, q, k, v) with q/k/v as the kernels read them."""
+def attention_forward(q, k, v, sm_scale, family, window=0, documents_idx_BxT=None, persistent_key_window=None,
+                      keep_layout=False):
+    """Runs the forward kernel; returns (o, lse, q, k, v, workspace) with q/k/v as the kernels read them.
+
+    With ``keep_layout`` (and documents) the workspace is sized for the backward and keeps the document
+    row layout the forward computed; pass it to ``attention_backward(layout_workspace=...)`` so the
+    backward skips recomputing it."""
     q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
     b, h, n, d = q.shape
     o = _alloc_like_bnhd(q)
     lse = torch.empty((b, h, n), dtype=torch.float32, device=q.device)
     docs_ptr, docs_code, docs_sb = _docs_args(documents_idx_BxT)
-    ws = _workspace(family, b, h, n, documents_idx_BxT is not None, False, q.device)
+    keep = bool(keep_layout) and documents_idx_BxT is not None
+    ws = _workspace(family, b, h, n, documents_idx_BxT is not None, keep, q.device)
     has_pkw = persistent_key_window is not None
     status = N.lib().sps_attn_fwd(
         family, b, h, n, d, _dtype_code(q),
@@ -113,23 +119,26 @@ def attention_forward(q, k, v, sm_scale, family, window=0, documents_idx_BxT=Non
         ws.data_ptr(), ws.numel(), _stream(q),
     )
     N.check("sps_attn_fwd", status)
-    return o, lse, q, k, v
+    return o, lse, q, k, v, (ws if keep else None)
 
 
 def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, documents_idx_BxT=None,
-                       persistent_key_window=None, between_passes=None):
+                       persistent_key_window=None, between_passes=None, layout_workspace=None):
     """Runs the backward kernels; returns (dq, dk, dv) laid out like q, k, v.
 
     ``between_passes``: optional callable run on the host after the dQ pass is enqueued and before the
     dK/dV pass (e.g. to record a torch.cuda.Event on the current stream for per-kernel timing); the two
-    passes are then launched through sps_attn_bwd_pass instead of one sps_attn_bwd call."""
+    passes are then launched separately. ``layout_workspace``: the workspace returned by
+    ``attention_forward(keep_layout=True)`` for the same arguments; the backward then reuses its
+    document layout instead of recomputing it."""
     do = _kernel_view(do)
     b, h, n, d = q.shape
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     docs_ptr, docs_code, docs_sb = _docs_args(documents_idx_BxT)
-    ws = _workspace(family, b, h, n, documents_idx_BxT is not None, True, q.device)
+    reuse = layout_workspace is not None and documents_idx_BxT is not None
+    ws = layout_workspace if reuse else _workspace(family, b, h, n, documents_idx_BxT is not None, True, q.device)
     has_pkw = persistent_key_window is not None
     args = (
         family, b, h, n, d, _dtype_code(q),
@@ -140,12 +149,14 @@ def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, document
         float(sm_scale), int(window), int(has_pkw), int(persistent_key_window) if has_pkw else -1,
         ws.data_ptr(), ws.numel(), _stream(q),
     )
+    lib = N.lib()
+    reuse_bit = N.BWD_REUSE_LAYOUT if reuse else 0
     if between_passes is None:
-        N.check("sps_attn_bwd", N.lib().sps_attn_bwd(*args))
+        N.check("sps_attn_bwd_pass", lib.sps_attn_bwd_pass(N.BWD_DQ | N.BWD_DKDV | reuse_bit, *args))
     else:
-        N.check("sps_attn_bwd_pass", N.lib().sps_attn_bwd_pass(N.BWD_DQ, *args))
+        N.check("sps_attn_bwd_pass", lib.sps_attn_bwd_pass(N.BWD_DQ | reuse_bit, *args))
         between_passes()
-        N.check("sps_attn_bwd_pass", N.lib().sps_attn_bwd_pass(N.BWD_DKDV, *args))
+        N.check("sps_attn_bwd_pass", lib.sps_attn_bwd_pass(N.BWD_DKDV, *args))
     return dq, dk, dv
 
 
@@ -153,9 +164,11 @@ class _Attention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, sm_scale, family, window, documents_idx_BxT, persistent_key_window):
         _validate(q, k, v, family, documents_idx_BxT)
-        o, lse, qk, kk, vk = attention_forward(
-            q, k, v, sm_scale, family, window, documents_idx_BxT, persistent_key_window
+        needs_grad = any(t.requires_grad for t in (q, k, v))
+        o, lse, qk, kk, vk, ws = attention_forward(
+            q, k, v, sm_scale, family, window, documents_idx_BxT, persistent_key_window, keep_layout=needs_grad
         )
+        ctx.layout_ws = ws
         if documents_idx_BxT is not None:
             ctx.save_for_backward(qk, kk, vk, o, lse, documents_idx_BxT)
         else:
@@ -175,8 +188,9 @@ class _Attention(torch.autograd.Function):
             q, k, v, o, lse = ctx.saved_tensors
             docs = None
         dq, dk, dv = attention_backward(
-            do, q, k, v, o, lse, ctx.sm_scale, ctx.family, ctx.window, docs, ctx.pkw
+            do, q, k, v, o, lse, ctx.sm_scale, ctx.family, ctx.window, docs, ctx.pkw, layout_workspace=ctx.layout_ws
         )
+        ctx.layout_ws = None
         return dq, dk, dv, None, None, None, None, None
 
 

@@ -14,19 +14,21 @@
 //     keys: the w-token window):
 //       S = Q K^T, dP = dO V^T (Q, dO rows from LDS; K, V in registers),
 //       dV^T += dO^T P, dK^T += Q^T dS (dO^T, Q^T fragments via ds_read_b64_tr_b16).
-// Both passes stream their tiles through a ring of R register sets into double-buffered LDS tiles
-// (loads issued R blocks ahead, one barrier per block). dK and dQ are scaled by sm_scale at the
+// Both passes consume their tiles in pairs of 32-row blocks (one barrier per pair) through the
+// run_pairs pipeline: buffer loads one pair ahead into registers, double-buffered LDS. dK and dQ are scaled by sm_scale at the
 // end, as in the reference.
 #include "attn_tiles.hpp"
 
 namespace sps {
 
-template <int D, class E, int R>
+// Pairs of blocks whose loads are in flight while a pair is computed (run_pairs).
+constexpr int kLook = 1;
+
+template <int D, class E>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
-  static_assert(R % 2 == 0, "the register ring depth must be even (static LDS buffer indices)");
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][G::ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][2][G::ELEMS];  // [buffer][block of the pair]
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][2][G::ELEMS];
   __shared__ int s_span[4 * kWaves];
 
   const MaskSpec m = a.m;
@@ -45,8 +47,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   const bool exact = row.mono;
   const int64_t dq_doc = (!exact && qvalid) ? load_doc(a, b, qp) : 0;
 
-  const uint16_t* kbase = a.k + b * a.sk.b + h * a.sk.h;
-  const uint16_t* vbase = a.v + b * a.sv.b + h * a.sv.h;
+  const BufRsrc k_src = head_rsrc<D>(a.k + b * a.sk.b + h * a.sk.h, a.sk.n, m.N);
+  const BufRsrc v_src = head_rsrc<D>(a.v + b * a.sv.b + h * a.sv.h, a.sv.n, m.N);
+  const int step = m.family == FAMILY_FULL ? 1 : 2;  // positions between consecutive stream rows
+  const auto k_off = TileRegs<D>::offsets(tid, (uint32_t)(step * a.sk.n * 2));
+  const auto v_off = TileRegs<D>::offsets(tid, (uint32_t)(step * a.sv.n * 2));
 
   // Q and dO fragments (B operands; lane: query c32, d = 16c + 8g .. +7) and Delta.
   u32x4_t qf[D / 16], dof[D / 16];
@@ -72,92 +77,83 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   }
   const int64_t rowid = ((int64_t)b * a.H + h) * m.N + qsafe;
   if (qvalid && g == 0) a.delta[rowid] = delta;
-  const float lse = qvalid ? a.lse[rowid] : 0.f;
-
-  zero_pad_cols<D>(sK[0], tid);
-  zero_pad_cols<D>(sK[1], tid);
-  zero_pad_cols<D>(sV[0], tid);
-  zero_pad_cols<D>(sV[1], tid);
-
-  TileRegs<D> rk[R], rv[R];
-  auto issue = [&](int i, TileRegs<D>& tk, TileRegs<D>& tv) {
-    const int s = plan.stream(i);
-    const int pos0 = stream_pos(m, s, plan.first(i));
-    const int step = s == STREAM_NATURAL ? 1 : 2;
-    tk.load(kbase, a.sk.n, m.N, tid, pos0, step);
-    tv.load(vbase, a.sv.n, m.N, tid, pos0, step);
-  };
+  float lse = qvalid ? a.lse[rowid] : 0.f;
+  lse = lse == -INFINITY ? 0.f : lse;  // a query with no visible key: every score is masked to -inf
 
 #pragma unroll
-  for (int j = 0; j < R; ++j)
-    if (j < nb) issue(j, rk[j], rv[j]);
-  if (nb > 0) {
-    rk[0].store(sK[0], tid);
-    rv[0].store(sV[0], tid);
+  for (int x = 0; x < 2; ++x) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      zero_pad_cols<D>(sK[x][y], tid);
+      zero_pad_cols<D>(sV[x][y], tid);
+    }
   }
-  if (R < nb) issue(R, rk[0], rv[0]);
-  __syncthreads();
+
+  TileRegs<D> rk[kLook][2], rv[kLook][2];
+  auto issue = [&](int j, int slot) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int i = 2 * j + y;
+      if (i < nb) {
+        const int pos0 = stream_pos(m, plan.stream(i), plan.first(i));
+        rk[slot][y].load(k_src, (uint32_t)(pos0 * a.sk.n * 2), k_off, tid);
+        rv[slot][y].load(v_src, (uint32_t)(pos0 * a.sv.n * 2), v_off, tid);
+      }
+    }
+  };
+  auto put = [&](int slot, int buf) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      rk[slot][y].store(sK[buf][y], tid);
+      rv[slot][y].store(sV[buf][y], tid);
+    }
+  };
 
   f32x16_t acc[G::DC];
 #pragma unroll
   for (int dc = 0; dc < G::DC; ++dc) acc[dc] = f32x16_t{};
 
-  vmem_wait_all();
-  // Two copies of the loop: exact interval masks (ids non-decreasing), or interval + id checks.
   auto run = [&](auto exact_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
-    for (int i0 = 0; i0 < nb; i0 += R) {
+    run_pairs<kLook>(nb, issue, put, [&](int j, int buf) {
 #pragma unroll
-      for (int u = 0; u < R; ++u) {
-        const int i = i0 + u;
-        if (i < nb) {
-          const int nslot = (u + 1) % R;
-          if (i + 1 < nb) {
-            rk[nslot].store(sK[(u + 1) & 1], tid);
-            rv[nslot].store(sV[(u + 1) & 1], tid);
+      for (int y = 0; y < 2; ++y) {
+        const int i = 2 * j + y;
+        const bool s0 = i < plan.n0;
+        const int t0 = plan.first(i);
+        const WaveSpan ws = s0 ? st.w0 : st.w1;
+        const Interval lr = s0 ? st.r0 : st.r1;
+        const int cls = i < nb ? classify_block(ws, t0, EXACT) : TILE_SKIP;
+        if (cls != TILE_SKIP) {
+          const uint16_t* tK = sK[buf][y];
+          const uint16_t* tV = sV[buf][y];
+          f32x16_t sc = {}, dp = {};
+#pragma unroll
+          for (int c = 0; c < D / 16; ++c) {
+            sc = E::mfma(lds_read_b128(tK + c32 * G::RS + 16 * c + 8 * g), qf[c], sc);
+            dp = E::mfma(lds_read_b128(tV + c32 * G::RS + 16 * c + 8 * g), dof[c], dp);
           }
-          if (i + 1 + R < nb) issue(i + 1 + R, rk[nslot], rv[nslot]);
-
-          const bool s0 = i < plan.n0;
-          const int t0 = plan.first(i);
-          const WaveSpan ws = s0 ? st.w0 : st.w1;
-          const Interval lr = s0 ? st.r0 : st.r1;
-          const int cls = classify_block(ws, t0, EXACT);
-          if (cls != TILE_SKIP) {
-            const uint16_t* tK = sK[u & 1];
-            const uint16_t* tV = sV[u & 1];
-            f32x16_t sc = {}, dp = {};
+          if (cls == TILE_PARTIAL)
+            mask_partial<EXACT>(sc, lr, ws, t0, g,
+                                [&] { return qs_exact_bits(a, b, lr, plan.stream(i), t0, g, dq_doc); });
+          uint32_t dsk[8];
 #pragma unroll
-            for (int c = 0; c < D / 16; ++c) {
-              sc = E::mfma(lds_read_b128(tK + c32 * G::RS + 16 * c + 8 * g), qf[c], sc);
-              dp = E::mfma(lds_read_b128(tV + c32 * G::RS + 16 * c + 8 * g), dof[c], dp);
-            }
-            uint32_t bits = 0xffffu;
-            if (cls == TILE_PARTIAL)
-              bits = EXACT ? interval_keep_bits(lr.lo, lr.hi, t0, g)
-                           : qs_exact_bits(a, b, lr, plan.stream(i), t0, g, dq_doc);
-            uint32_t dsk[8];
+          for (int e = 0; e < 8; ++e) {
+            const float p0 = fast_exp2(fmaf(sc[2 * e], a.scale2, -lse));
+            const float p1 = fast_exp2(fmaf(sc[2 * e + 1], a.scale2, -lse));
+            dsk[e] = E::pack2(p0 * (dp[2 * e] - delta), p1 * (dp[2 * e + 1] - delta));
+          }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              float p0 = fast_exp2(fmaf(sc[2 * j], a.scale2, -lse));
-              float p1 = fast_exp2(fmaf(sc[2 * j + 1], a.scale2, -lse));
-              p0 = ((bits >> (2 * j)) & 1u) ? p0 : 0.f;
-              p1 = ((bits >> (2 * j + 1)) & 1u) ? p1 : 0.f;
-              dsk[j] = E::pack2(p0 * (dp[2 * j] - delta), p1 * (dp[2 * j + 1] - delta));
-            }
+          for (int dc = 0; dc < G::DC; ++dc) {
 #pragma unroll
-            for (int dc = 0; dc < G::DC; ++dc) {
-#pragma unroll
-              for (int kh = 0; kh < 2; ++kh) {
-                const u32x4_t df = {dsk[4 * kh], dsk[4 * kh + 1], dsk[4 * kh + 2], dsk[4 * kh + 3]};
-                acc[dc] = E::mfma(lds_frag_tr(tK, G::RS, 16 * kh, 32 * dc, lane), df, acc[dc]);
-              }
+            for (int kh = 0; kh < 2; ++kh) {
+              const u32x4_t df = {dsk[4 * kh], dsk[4 * kh + 1], dsk[4 * kh + 2], dsk[4 * kh + 3]};
+              acc[dc] = E::mfma(lds_frag_tr(tK, G::RS, 16 * kh, 32 * dc, lane), df, acc[dc]);
             }
           }
-          __syncthreads();
         }
       }
-    }
+    });
   };
   if (exact)
     run(std::true_type{});
@@ -189,14 +185,13 @@ struct ChunkRegs {
   float lse, delta;
 };
 
-template <int D, class E, int R>
+template <int D, class E>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
-  static_assert(R % 2 == 0, "the register ring depth must be even (static LDS buffer indices)");
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t sDO[2][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) float sLse[2][kBlock];
-  __shared__ __attribute__((aligned(16))) float sDelta[2][kBlock];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][2][G::ELEMS];  // [buffer][chunk of the pair]
+  __shared__ __attribute__((aligned(16))) uint16_t sDO[2][2][G::ELEMS];
+  __shared__ __attribute__((aligned(16))) float sLse[2][2][kBlock];
+  __shared__ __attribute__((aligned(16))) float sDelta[2][2][kBlock];
   __shared__ int s_span[2 * kWaves];
 
   const MaskSpec m = a.m;
@@ -213,8 +208,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   const bool exact = row.mono;
   const int64_t dk_doc = (!exact && kvalid) ? load_doc(a, b, kp) : 0;
 
-  const uint16_t* qbase = a.q + b * a.sq.b + h * a.sq.h;
-  const uint16_t* dobase = a.dO + b * a.sdo.b + h * a.sdo.h;
+  const BufRsrc q_src = head_rsrc<D>(a.q + b * a.sq.b + h * a.sq.h, a.sq.n, m.N);
+  const BufRsrc o_src = head_rsrc<D>(a.dO + b * a.sdo.b + h * a.sdo.h, a.sdo.n, m.N);
+  const auto q_off = TileRegs<D>::offsets(tid, (uint32_t)(a.sq.n * 2));
+  const auto o_off = TileRegs<D>::offsets(tid, (uint32_t)(a.sdo.n * 2));
   const float* lse_row = a.lse + ((int64_t)b * a.H + h) * m.N;
   const float* delta_row = a.delta + ((int64_t)b * a.H + h) * m.N;
 
@@ -231,37 +228,44 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
     }
   }
 
-  zero_pad_cols<D>(sQ[0], tid);
-  zero_pad_cols<D>(sQ[1], tid);
-  zero_pad_cols<D>(sDO[0], tid);
-  zero_pad_cols<D>(sDO[1], tid);
-
-  ChunkRegs<D> rc[R];
-  auto issue = [&](int i, ChunkRegs<D>& c) {
-    const int q0 = (st.c0 + i) * kBlock;
-    c.q.load(qbase, a.sq.n, m.N, tid, q0, 1);
-    c.o.load(dobase, a.sdo.n, m.N, tid, q0, 1);
-    if (tid < kBlock) {
-      const int qp = imin(q0 + tid, m.N - 1);
-      c.lse = lse_row[qp];
-      c.delta = delta_row[qp];
-    }
-  };
-  auto put = [&](const ChunkRegs<D>& c, int buf) {
-    c.q.store(sQ[buf], tid);
-    c.o.store(sDO[buf], tid);
-    if (tid < kBlock) {
-      sLse[buf][tid] = c.lse;
-      sDelta[buf][tid] = c.delta;
-    }
-  };
-
 #pragma unroll
-  for (int j = 0; j < R; ++j)
-    if (j < nc) issue(j, rc[j]);
-  if (nc > 0) put(rc[0], 0);
-  if (R < nc) issue(R, rc[0]);
-  __syncthreads();
+  for (int x = 0; x < 2; ++x) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      zero_pad_cols<D>(sQ[x][y], tid);
+      zero_pad_cols<D>(sDO[x][y], tid);
+    }
+  }
+
+  ChunkRegs<D> rc[kLook][2];
+  auto issue = [&](int j, int slot) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int i = 2 * j + y;
+      if (i < nc) {
+        const int q0 = (st.c0 + i) * kBlock;
+        rc[slot][y].q.load(q_src, (uint32_t)(q0 * a.sq.n * 2), q_off, tid);
+        rc[slot][y].o.load(o_src, (uint32_t)(q0 * a.sdo.n * 2), o_off, tid);
+        if (tid < kBlock) {
+          const int qp = imin(q0 + tid, m.N - 1);
+          const float l = lse_row[qp];
+          rc[slot][y].lse = l == -INFINITY ? 0.f : l;  // a query with no visible key: its scores are all masked
+          rc[slot][y].delta = delta_row[qp];
+        }
+      }
+    }
+  };
+  auto put = [&](int slot, int buf) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      rc[slot][y].q.store(sQ[buf][y], tid);
+      rc[slot][y].o.store(sDO[buf][y], tid);
+      if (tid < kBlock) {
+        sLse[buf][y][tid] = rc[slot][y].lse;
+        sDelta[buf][y][tid] = rc[slot][y].delta;
+      }
+    }
+  };
 
   f32x16_t dk[G::DC], dv[G::DC];
 #pragma unroll
@@ -270,72 +274,59 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
     dv[dc] = f32x16_t{};
   }
 
-  vmem_wait_all();
-  // Two copies of the loop: exact interval masks (ids non-decreasing), or interval + id checks.
   auto run = [&](auto exact_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
-    for (int i0 = 0; i0 < nc; i0 += R) {
+    run_pairs<kLook>(nc, issue, put, [&](int j, int buf) {
 #pragma unroll
-      for (int u = 0; u < R; ++u) {
-        const int i = i0 + u;
-        if (i < nc) {
-          const int nslot = (u + 1) % R;
-          if (i + 1 < nc) put(rc[nslot], (u + 1) & 1);
-          if (i + 1 + R < nc) issue(i + 1 + R, rc[nslot]);
-
-          const int qc = (st.c0 + i) * kBlock;
-          const int cls = classify_block(st.w, qc, EXACT);
-          if (cls != TILE_SKIP) {
-            const int buf = u & 1;
-            const uint16_t* tQ = sQ[buf];
-            const uint16_t* tDO = sDO[buf];
-            f32x16_t sc = {}, dp = {};
+      for (int y = 0; y < 2; ++y) {
+        const int i = 2 * j + y;
+        const int qc = (st.c0 + i) * kBlock;
+        const int cls = i < nc ? classify_block(st.w, qc, EXACT) : TILE_SKIP;
+        if (cls != TILE_SKIP) {
+          const uint16_t* tQ = sQ[buf][y];
+          const uint16_t* tDO = sDO[buf][y];
+          f32x16_t sc = {}, dp = {};
 #pragma unroll
-            for (int c = 0; c < D / 16; ++c) {
-              sc = E::mfma(lds_read_b128(tQ + c32 * G::RS + 16 * c + 8 * g), kf[c], sc);
-              dp = E::mfma(lds_read_b128(tDO + c32 * G::RS + 16 * c + 8 * g), vf[c], dp);
+          for (int c = 0; c < D / 16; ++c) {
+            sc = E::mfma(lds_read_b128(tQ + c32 * G::RS + 16 * c + 8 * g), kf[c], sc);
+            dp = E::mfma(lds_read_b128(tDO + c32 * G::RS + 16 * c + 8 * g), vf[c], dp);
+          }
+          if (cls == TILE_PARTIAL)
+            mask_partial<EXACT>(sc, st.r, st.w, qc, g,
+                                [&] { return ks_exact_bits(a, b, kp, st.r.hi, qc, g, dk_doc); });
+          uint32_t pk[8], dsk[8];
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) {
+            // Query rows 8*i4 + 4g + {0..3} of this chunk.
+            const f32x4_t l4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
+                (const SPS_LDS float*)(&sLse[buf][y][8 * i4 + 4 * g]));
+            const f32x4_t d4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
+                (const SPS_LDS float*)(&sDelta[buf][y][8 * i4 + 4 * g]));
+            float p[4], ds[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const int e = 4 * i4 + t;
+              p[t] = fast_exp2(fmaf(sc[e], a.scale2, -l4[t]));
+              ds[t] = p[t] * (dp[e] - d4[t]);
             }
-            uint32_t bits = 0xffffu;
-            if (cls == TILE_PARTIAL)
-              bits = EXACT ? interval_keep_bits(st.r.lo, st.r.hi, qc, g)
-                           : ks_exact_bits(a, b, kp, st.r.hi, qc, g, dk_doc);
-            uint32_t pk[8], dsk[8];
+            pk[2 * i4] = E::pack2(p[0], p[1]);
+            pk[2 * i4 + 1] = E::pack2(p[2], p[3]);
+            dsk[2 * i4] = E::pack2(ds[0], ds[1]);
+            dsk[2 * i4 + 1] = E::pack2(ds[2], ds[3]);
+          }
 #pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {
-              // Query rows 8*i4 + 4g + {0..3} of this chunk.
-              const f32x4_t l4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                  (const SPS_LDS float*)(&sLse[buf][8 * i4 + 4 * g]));
-              const f32x4_t d4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                  (const SPS_LDS float*)(&sDelta[buf][8 * i4 + 4 * g]));
-              float p[4], ds[4];
+          for (int dc = 0; dc < G::DC; ++dc) {
 #pragma unroll
-              for (int t = 0; t < 4; ++t) {
-                const int e = 4 * i4 + t;
-                float pv = fast_exp2(fmaf(sc[e], a.scale2, -l4[t]));
-                pv = ((bits >> e) & 1u) ? pv : 0.f;
-                p[t] = pv;
-                ds[t] = pv * (dp[e] - d4[t]);
-              }
-              pk[2 * i4] = E::pack2(p[0], p[1]);
-              pk[2 * i4 + 1] = E::pack2(p[2], p[3]);
-              dsk[2 * i4] = E::pack2(ds[0], ds[1]);
-              dsk[2 * i4 + 1] = E::pack2(ds[2], ds[3]);
-            }
-#pragma unroll
-            for (int dc = 0; dc < G::DC; ++dc) {
-#pragma unroll
-              for (int kh = 0; kh < 2; ++kh) {
-                const u32x4_t pf = {pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]};
-                const u32x4_t df = {dsk[4 * kh], dsk[4 * kh + 1], dsk[4 * kh + 2], dsk[4 * kh + 3]};
-                dv[dc] = E::mfma(lds_frag_tr(tDO, G::RS, 16 * kh, 32 * dc, lane), pf, dv[dc]);
-                dk[dc] = E::mfma(lds_frag_tr(tQ, G::RS, 16 * kh, 32 * dc, lane), df, dk[dc]);
-              }
+            for (int kh = 0; kh < 2; ++kh) {
+              const u32x4_t pf = {pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]};
+              const u32x4_t df = {dsk[4 * kh], dsk[4 * kh + 1], dsk[4 * kh + 2], dsk[4 * kh + 3]};
+              dv[dc] = E::mfma(lds_frag_tr(tDO, G::RS, 16 * kh, 32 * dc, lane), pf, dv[dc]);
+              dk[dc] = E::mfma(lds_frag_tr(tQ, G::RS, 16 * kh, 32 * dc, lane), df, dk[dc]);
             }
           }
-          __syncthreads();
         }
       }
-    }
+    });
   };
   if (exact)
     run(std::true_type{});
@@ -382,8 +373,16 @@ __global__ __launch_bounds__(256) void mask_dump_kv_kernel(const AttnArgs a) {
     const int cls = classify_block(st.w, qc, exact);
     if (cls == TILE_SKIP || !st.kvalid) continue;
     uint32_t bits = 0xffffu;
-    if (cls == TILE_PARTIAL)
-      bits = exact ? interval_keep_bits(st.r.lo, st.r.hi, qc, g) : ks_exact_bits(a, b, st.kp, st.r.hi, qc, g, dk_doc);
+    if (cls == TILE_PARTIAL) {
+      f32x16_t z = {};
+      auto exact_bits = [&] { return ks_exact_bits(a, b, st.kp, st.r.hi, qc, g, dk_doc); };
+      if (exact)
+        mask_partial<true>(z, st.r, st.w, qc, g, exact_bits);
+      else
+        mask_partial<false>(z, st.r, st.w, qc, g, exact_bits);
+      bits = 0;
+      for (int e = 0; e < 16; ++e) bits |= (uint32_t)(z[e] == 0.f) << e;
+    }
     for (int e = 0; e < 16; ++e) {
       const int qp = qc + acc_row(e, g);
       if (((bits >> e) & 1u) && qp < m.N) a.mask_out[((int64_t)b * m.N + qp) * m.N + st.kp] = 1;
@@ -396,12 +395,12 @@ static hipError_t launch_bwd_t(const AttnArgs& a, int passes, hipStream_t stream
   const int64_t nq = (int64_t)q_tiles(a.m.N) * a.B * a.H;
   const int64_t nk = (int64_t)k_tiles(a.m.family, a.m.N, a.m.P) * a.B * a.H;
   if ((passes & kBwdDq) && nq > 0) {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, E, 2>), dim3((unsigned)nq), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, E>), dim3((unsigned)nq), dim3(256), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if ((passes & kBwdDkdv) && nk > 0) {
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, E, 2>), dim3((unsigned)nk), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<D, E>), dim3((unsigned)nk), dim3(256), 0, stream, a);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -10,8 +10,9 @@
 // Schedule: the workgroup's key blocks are the union of its lanes' visible intervals (one range of
 // 32-row blocks per key stream, computed once from the prepass's run starts), and each wave
 // classifies each block from four numbers (attn_sched.hpp), so no per-block lookups go to memory.
-// K/V blocks flow global -> registers -> LDS through a ring of R register sets: a block's loads are
-// issued R blocks before it is computed, the LDS tiles are double-buffered, one barrier per block.
+// K/V blocks are consumed in pairs (64 rows, one barrier per pair) through the run_pairs pipeline:
+// buffer loads into registers one pair ahead, double-buffered LDS tiles; rows past the end of the
+// sequence read as zeros.
 //
 // Softmax: exp2 domain with log2(e) folded into the scale; the running max is only raised (and the
 // accumulator rescaled) when a block's max exceeds it by more than 2^8, so P stays <= 256 and most
@@ -24,14 +25,16 @@
 
 namespace sps {
 
+// Pairs of blocks whose loads are in flight while a pair is computed (run_pairs).
+constexpr int kLook = 1;
+
 constexpr float kRescaleThreshold = 8.0f;
 
-template <int D, class E, int R>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
+template <int D, class E>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 2, 8))) void attn_fwd_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
-  static_assert(R % 2 == 0, "the register ring depth must be even (static LDS buffer indices)");
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][G::ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][2][G::ELEMS];  // [buffer][block of the pair]
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][2][G::ELEMS];
   __shared__ int s_span[4 * kWaves];
 
   const MaskSpec m = a.m;
@@ -49,8 +52,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
   const bool exact = row.mono;
   const int64_t dq_doc = (!exact && qvalid) ? load_doc(a, b, qp) : 0;
 
-  const uint16_t* kbase = a.k + b * a.sk.b + h * a.sk.h;
-  const uint16_t* vbase = a.v + b * a.sv.b + h * a.sv.h;
+  const BufRsrc k_src = head_rsrc<D>(a.k + b * a.sk.b + h * a.sk.h, a.sk.n, m.N);
+  const BufRsrc v_src = head_rsrc<D>(a.v + b * a.sv.b + h * a.sv.h, a.sv.n, m.N);
+  const int step = m.family == FAMILY_FULL ? 1 : 2;  // positions between consecutive stream rows
+  const auto k_off = TileRegs<D>::offsets(tid, (uint32_t)(step * a.sk.n * 2));
+  const auto v_off = TileRegs<D>::offsets(tid, (uint32_t)(step * a.sv.n * 2));
 
   // Q fragments: B operand of S^T = K Q^T (lane: query c32, d = 16c + 8g .. +7).
   u32x4_t qf[D / 16];
@@ -63,107 +69,117 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
     }
   }
 
-  zero_pad_cols<D>(sK[0], tid);
-  zero_pad_cols<D>(sK[1], tid);
-  zero_pad_cols<D>(sV[0], tid);
-  zero_pad_cols<D>(sV[1], tid);
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      zero_pad_cols<D>(sK[x][y], tid);
+      zero_pad_cols<D>(sV[x][y], tid);
+    }
+  }
 
-  TileRegs<D> rk[R], rv[R];
-  auto issue = [&](int i, TileRegs<D>& tk, TileRegs<D>& tv) {
-    const int s = plan.stream(i);
-    const int pos0 = stream_pos(m, s, plan.first(i));
-    const int step = s == STREAM_NATURAL ? 1 : 2;
-    tk.load(kbase, a.sk.n, m.N, tid, pos0, step);
-    tv.load(vbase, a.sv.n, m.N, tid, pos0, step);
+  // Byte offset of block i's first row: i * (bytes per block) + a per-stream constant.
+  const uint32_t k_blk = (uint32_t)(kBlock * step * a.sk.n * 2), v_blk = (uint32_t)(kBlock * step * a.sv.n * 2);
+  const int c0 = stream_pos(m, plan.stream0, kBlock * plan.b0);
+  const int c1 = m.family == FAMILY_FULL ? 0 : stream_pos(m, STREAM_TEMPORARY, kBlock * plan.b1) - kBlock * step * plan.n0;
+  const uint32_t k_c0 = (uint32_t)(c0 * a.sk.n * 2), k_c1 = (uint32_t)(c1 * a.sk.n * 2);
+  const uint32_t v_c0 = (uint32_t)(c0 * a.sv.n * 2), v_c1 = (uint32_t)(c1 * a.sv.n * 2);
+
+  TileRegs<D> rk[kLook][2], rv[kLook][2];
+  auto issue = [&](int j, int slot) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int i = 2 * j + y;
+      if (i < nb) {
+        const bool s0 = i < plan.n0;
+        rk[slot][y].load(k_src, (uint32_t)i * k_blk + (s0 ? k_c0 : k_c1), k_off, tid);
+        rv[slot][y].load(v_src, (uint32_t)i * v_blk + (s0 ? v_c0 : v_c1), v_off, tid);
+      }
+    }
+  };
+  auto put = [&](int slot, int buf) {
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      rk[slot][y].store(sK[buf][y], tid);
+      rv[slot][y].store(sV[buf][y], tid);
+    }
   };
 
-#pragma unroll
-  for (int j = 0; j < R; ++j)
-    if (j < nb) issue(j, rk[j], rv[j]);
-  if (nb > 0) {
-    rk[0].store(sK[0], tid);
-    rv[0].store(sV[0], tid);
-  }
-  if (R < nb) issue(R, rk[0], rv[0]);
-  __syncthreads();
-
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_run = -INFINITY, l_run[4] = {0.f, 0.f, 0.f, 0.f};
   f32x16_t acc[G::DC];
 #pragma unroll
   for (int dc = 0; dc < G::DC; ++dc) acc[dc] = f32x16_t{};
 
-  vmem_wait_all();
-  // Two copies of the loop: exact interval masks (ids non-decreasing), or interval + id checks.
+  // One pair = two 32-row key blocks: both score tiles, one joint max / rescale decision, PV for both.
+  // The score tiles are computed for both blocks whenever the pair has work for this wave (a skipped
+  // block is masked to -inf instead of branched around), and masks run only in pairs that have a
+  // partial block: few branches, so the compiler can interleave the MFMA and VALU work.
   auto run = [&](auto exact_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
-    for (int i0 = 0; i0 < nb; i0 += R) {
+    auto cls_of = [&](int i) {
+      return classify_block(i < plan.n0 ? st.w0 : st.w1, plan.first(i), EXACT);
+    };
+    const BlockMask bm = build_block_mask(nb, cls_of);
+    run_pairs<kLook>(nb, issue, put, [&](int j, int buf) {
+      int act2, full2;
+      pair_codes(bm, 2 * j, nb, cls_of, act2, full2);
+      if (act2 == 0) return;
+      f32x16_t sc[2];
 #pragma unroll
-      for (int u = 0; u < R; ++u) {
-        const int i = i0 + u;
-        if (i < nb) {
-          const int nslot = (u + 1) % R;
-          if (i + 1 < nb) {
-            rk[nslot].store(sK[(u + 1) & 1], tid);
-            rv[nslot].store(sV[(u + 1) & 1], tid);
+      for (int y = 0; y < 2; ++y) {
+        const uint16_t* tK = sK[buf][y];
+        sc[y] = E::mfma(lds_read_b128(tK + c32 * G::RS + 8 * g), qf[0], f32x16_t{});
+#pragma unroll
+        for (int c = 1; c < D / 16; ++c)
+          sc[y] = E::mfma(lds_read_b128(tK + c32 * G::RS + 16 * c + 8 * g), qf[c], sc[y]);
+      }
+      if (full2 != 3) {
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+          if (!((act2 >> y) & 1)) {
+            sc[y] = f32x16_t{} - INFINITY;
+          } else if (!((full2 >> y) & 1)) {
+            const int i = 2 * j + y;
+            const bool s0 = i < plan.n0;
+            const int t0 = plan.first(i);
+            const Interval lr = s0 ? st.r0 : st.r1;
+            mask_partial<EXACT>(sc[y], lr, s0 ? st.w0 : st.w1, t0, g,
+                                [&] { return qs_exact_bits(a, b, lr, plan.stream(i), t0, g, dq_doc); });
           }
-          if (i + 1 + R < nb) issue(i + 1 + R, rk[nslot], rv[nslot]);
-
-          const bool s0 = i < plan.n0;
-          const int t0 = plan.first(i);
-          const WaveSpan ws = s0 ? st.w0 : st.w1;
-          const Interval lr = s0 ? st.r0 : st.r1;
-          const int cls = classify_block(ws, t0, EXACT);
-          if (cls != TILE_SKIP) {
-            const uint16_t* tK = sK[u & 1];
-            const uint16_t* tV = sV[u & 1];
-            f32x16_t sc = {};
-#pragma unroll
-            for (int c = 0; c < D / 16; ++c)
-              sc = E::mfma(lds_read_b128(tK + c32 * G::RS + 16 * c + 8 * g), qf[c], sc);
-            if (cls == TILE_PARTIAL) {
-              if constexpr (EXACT) {
-                mask_outside(sc, lr.lo, lr.hi, t0, g);
-              } else {
-                const uint32_t bits = qs_exact_bits(a, b, lr, plan.stream(i), t0, g, dq_doc);
-#pragma unroll
-                for (int e = 0; e < 16; ++e) sc[e] = ((bits >> e) & 1u) ? sc[e] : -INFINITY;
-              }
-            }
-            float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
-#pragma unroll
-            for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, sc[e]), sc[e + 1]);
-            mx = fmaxf(mx, sc[15]);
-            const float mb = half_max(mx) * a.scale2;
-            const bool need = mb > m_run + kRescaleThreshold;
-            if (wave_any(need)) {
-              const float alpha = need ? fast_exp2(m_run - mb) : 1.f;
-              m_run = need ? mb : m_run;
-              l_run *= alpha;
-#pragma unroll
-              for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
-            }
-            const float mu = m_run == -INFINITY ? 0.f : m_run;
-            uint32_t pk[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const float p0 = fast_exp2(fmaf(sc[2 * j], a.scale2, -mu));
-              const float p1 = fast_exp2(fmaf(sc[2 * j + 1], a.scale2, -mu));
-              pk[j] = E::pack2(p0, p1);
-              l_run = E::sum2(pk[j], l_run);
-            }
-#pragma unroll
-            for (int dc = 0; dc < G::DC; ++dc) {
-#pragma unroll
-              for (int kh = 0; kh < 2; ++kh) {
-                const u32x4_t pf = {pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]};
-                acc[dc] = E::mfma(lds_frag_tr(tV, G::RS, 16 * kh, 32 * dc, lane), pf, acc[dc]);
-              }
-            }
-          }
-          __syncthreads();
         }
       }
-    }
+      const float mb = half_max(max32(sc[0], sc[1])) * a.scale2;
+      const bool need = mb > m_run + kRescaleThreshold;
+      if (wave_any(need)) {
+        const float alpha = need ? fast_exp2(m_run - mb) : 1.f;
+        m_run = need ? mb : m_run;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) l_run[r] *= alpha;
+#pragma unroll
+        for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
+      }
+      const float mu = m_run == -INFINITY ? 0.f : m_run;
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        uint32_t pk[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float p0 = fast_exp2(fmaf(sc[y][2 * e], a.scale2, -mu));
+          const float p1 = fast_exp2(fmaf(sc[y][2 * e + 1], a.scale2, -mu));
+          pk[e] = E::pack2(p0, p1);
+          l_run[e & 3] = E::sum2(pk[e], l_run[e & 3]);  // four independent partial sums
+        }
+        const uint16_t* tV = sV[buf][y];
+#pragma unroll
+        for (int dc = 0; dc < G::DC; ++dc) {
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh) {
+            const u32x4_t pf = {pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]};
+            acc[dc] = E::mfma(lds_frag_tr(tV, G::RS, 16 * kh, 32 * dc, lane), pf, acc[dc]);
+          }
+        }
+      }
+    });
   };
   if (exact)
     run(std::true_type{});
@@ -171,7 +187,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
     run(std::false_type{});
 
   // Epilogue: combine the two halves' partial sums, normalise, store O (lane = query row) and LSE.
-  const float l_tot = half_sum(l_run);
+  const float l_tot = half_sum((l_run[0] + l_run[1]) + (l_run[2] + l_run[3]));
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qvalid) {
     uint16_t* orow = a.out + b * a.sout.b + h * a.sout.h + (int64_t)qp * a.sout.n;
@@ -217,8 +233,16 @@ __global__ __launch_bounds__(256) void mask_dump_q_kernel(const AttnArgs a) {
     const int cls = classify_block(ws, t0, exact);
     if (cls == TILE_SKIP || !qvalid) continue;
     uint32_t bits = 0xffffu;
-    if (cls == TILE_PARTIAL)
-      bits = exact ? interval_keep_bits(lr.lo, lr.hi, t0, g) : qs_exact_bits(a, b, lr, stream, t0, g, dq_doc);
+    if (cls == TILE_PARTIAL) {
+      f32x16_t z = {};
+      auto exact_bits = [&] { return qs_exact_bits(a, b, lr, stream, t0, g, dq_doc); };
+      if (exact)
+        mask_partial<true>(z, lr, ws, t0, g, exact_bits);
+      else
+        mask_partial<false>(z, lr, ws, t0, g, exact_bits);
+      bits = 0;
+      for (int e = 0; e < 16; ++e) bits |= (uint32_t)(z[e] == 0.f) << e;
+    }
     for (int e = 0; e < 16; ++e) {
       if ((bits >> e) & 1u) mrow[stream_pos(m, stream, t0 + acc_row(e, g))] = 1;
     }
@@ -229,7 +253,7 @@ template <int D, class E>
 static hipError_t launch_fwd_t(const AttnArgs& a, hipStream_t stream) {
   const int64_t nblocks = (int64_t)q_tiles(a.m.N) * a.B * a.H;
   if (nblocks == 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, E, 2>), dim3((unsigned)nblocks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3((unsigned)nblocks), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -16,28 +16,39 @@ namespace sps {
 constexpr int kPrepThreads = 1024;
 constexpr int kRegIds = 8;  // ids per thread held in registers (rows up to kPrepThreads * kRegIds positions)
 constexpr int kMaxSortTiles = 2048;  // rows with more tiles keep the closed-form order
+constexpr int kLdsRow = kPrepThreads * kRegIds;  // rows up to this length keep their runs in LDS
 
 __device__ __forceinline__ int blocks_in(int lo, int hi) {
   return hi >= lo ? (hi >> 5) - (lo >> 5) + 1 : 0;
 }
 
+// Run bounds of a position, from the LDS copy (rows up to kLdsRow) or from global memory.
+struct RunBounds {
+  const short* s_lds;
+  const short* e_lds;
+  const int* s_glb;
+  const int* e_glb;
+  __device__ __forceinline__ int start(int p) const { return s_lds ? s_lds[p] : s_glb[p]; }
+  __device__ __forceinline__ int end(int p) const { return e_lds ? e_lds[p] : e_glb[p]; }
+};
+
 // Key blocks of the query tile qt (both streams), from its first and last queries' intervals.
-__device__ int q_tile_cost(const MaskSpec& m, const int* start, int qt) {
+__device__ int q_tile_cost(const MaskSpec& m, const RunBounds& rb, int qt) {
   const int qa = qt * kTile, qz = imin(qa + kTile - 1, m.N - 1);
   Interval a0, a1, z0, z1;
-  query_intervals(m, qa, start[qa], a0, a1);
-  query_intervals(m, qz, start[qz], z0, z1);
+  query_intervals(m, qa, rb.start(qa), a0, a1);
+  query_intervals(m, qz, rb.start(qz), z0, z1);
   return blocks_in(imin(a0.lo, z0.lo), imax(a0.hi, z0.hi)) + blocks_in(imin(a1.lo, z1.lo), imax(a1.hi, z1.hi));
 }
 
 // Query chunks of the key tile kt, from its first key and the last query of its last key.
-__device__ int k_tile_cost(const MaskSpec& m, const int* end, int kt) {
+__device__ int k_tile_cost(const MaskSpec& m, const RunBounds& rb, int kt) {
   int stream, first;
   k_tile_run(m, kt, stream, first);
   const int len = stream_len(m.family, m.N, stream, m.P);
   const int last = imin(first + kTile - 1, len - 1);
   const int k0 = stream_pos(m, stream, first), k1 = stream_pos(m, stream, last);
-  return blocks_in(k0, key_last_query(m, stream, k1, end[k1]));
+  return blocks_in(k0, key_last_query(m, stream, k1, rb.end(k1)));
 }
 
 // Exclusive scans over the per-thread chunk summaries (Hillis-Steele in LDS).
@@ -77,6 +88,7 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   __shared__ int s_scan[kPrepThreads];
   __shared__ int s_cost[kMaxSortTiles];
   __shared__ int s_nonmono;
+  __shared__ short s_start[kLdsRow], s_end[kLdsRow];
   const MaskSpec m = a.m;
   const int b = blockIdx.x, tid = threadIdx.x, N = m.N;
   int* start = a.run_start + (int64_t)b * N;
@@ -129,12 +141,18 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
 #pragma unroll
     for (int j = 0; j < kRegIds; ++j) {
       if (flag[j]) cur = p0 + j;
-      if (p0 + j < p1) start[p0 + j] = cur;
+      if (p0 + j < p1) {
+        start[p0 + j] = cur;
+        s_start[p0 + j] = (short)cur;
+      }
     }
     int nxt = carry_next;
 #pragma unroll
     for (int j = kRegIds - 1; j >= 0; --j) {
-      if (p0 + j < p1) end[p0 + j] = nxt - 1;
+      if (p0 + j < p1) {
+        end[p0 + j] = nxt - 1;
+        s_end[p0 + j] = (short)(nxt - 1);
+      }
       if (flag[j]) nxt = p0 + j;
     }
   } else if (mono) {
@@ -155,20 +173,27 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
     for (int p = p0; p < p1; ++p) {
       start[p] = 0;
       end[p] = N - 1;
+      if (in_regs) {
+        s_start[p] = 0;
+        s_end[p] = (short)(N - 1);
+      }
     }
   }
   if (tid == 0) a.row_mono[b] = mono ? 1 : 0;
   __syncthreads();  // start/end of the whole row are visible to every thread below
+  // Rows that fit read their run bounds from LDS (short: positions < kLdsRow <= 32767).
+  const bool lds_ok = in_regs;
+  const RunBounds rb = {lds_ok ? s_start : nullptr, lds_ok ? s_end : nullptr, start, end};
 
   const int nqt = q_tiles(N);
   if (nqt <= kMaxSortTiles)
-    for (int t = tid; t < nqt; t += kPrepThreads) s_cost[t] = q_tile_cost(m, start, t);
+    for (int t = tid; t < nqt; t += kPrepThreads) s_cost[t] = q_tile_cost(m, rb, t);
   __syncthreads();
   sort_tiles(s_cost, nqt, a.q_order + (int64_t)b * nqt, false);
   __syncthreads();
   const int nkt = k_tiles(m.family, N, m.P);
   if (nkt <= kMaxSortTiles)
-    for (int t = tid; t < nkt; t += kPrepThreads) s_cost[t] = k_tile_cost(m, end, t);
+    for (int t = tid; t < nkt; t += kPrepThreads) s_cost[t] = k_tile_cost(m, rb, t);
   __syncthreads();
   sort_tiles(s_cost, nkt, a.k_order + (int64_t)b * nkt, true);
 }

@@ -36,28 +36,38 @@ __device__ __forceinline__ void zero_pad_cols(uint16_t* tile, int tid) {
   }
 }
 
-// Register staging for one 32-row tile of a [B, H, N, D] tensor: row r is sequence position
-// pos0 + r * step, clamped to N - 1 (rows past the end are never visible, so their values only need
-// to be finite data of the same tensor).
+// Register staging for one 32-row tile of a [B, H, N, D] tensor read through a buffer descriptor
+// over one (batch, head) slice: row r of the tile is sequence position pos0 + r * step. Rows past
+// the end of the sequence read as zeros (they are never visible).
 template <int D>
 struct TileRegs {
-  u32x4_t v[TileGeom<D>::PASSES];
+  using G = TileGeom<D>;
+  u32x4_t v[G::PASSES];
 
-  __device__ __forceinline__ void load(const uint16_t* base, int64_t sn, int N, int tid, int pos0, int step) {
-    using G = TileGeom<D>;
+  // Byte offsets, from the tile's first row, of the 16-byte pieces this thread moves.
+  struct Offsets {
+    uint32_t o[G::PASSES];
+  };
+
+  static __device__ __forceinline__ Offsets offsets(int tid, uint32_t row_step_bytes) {
+    Offsets f;
 #pragma unroll
     for (int p = 0; p < G::PASSES; ++p) {
       const int r = p * G::RPP + tid / G::CPR;
-      const int ch = tid % G::CPR;
-      if (G::PASSES * G::RPP == kBlock || r < kBlock) {
-        const int kp = imin(pos0 + r * step, N - 1);
-        v[p] = *reinterpret_cast<const u32x4_t*>(base + (int64_t)kp * sn + ch * 8);
-      }
+      f.o[p] = (uint32_t)r * row_step_bytes + (uint32_t)(tid % G::CPR) * 16u;
+    }
+    return f;
+  }
+
+  __device__ __forceinline__ void load(BufRsrc rs, uint32_t first_row_bytes, const Offsets& f, int tid) {
+#pragma unroll
+    for (int p = 0; p < G::PASSES; ++p) {
+      const int r = p * G::RPP + tid / G::CPR;
+      if (G::PASSES * G::RPP == kBlock || r < kBlock) v[p] = buf_load_b128(rs, first_row_bytes + f.o[p]);
     }
   }
 
   __device__ __forceinline__ void store(uint16_t* tile, int tid) const {
-    using G = TileGeom<D>;
 #pragma unroll
     for (int p = 0; p < G::PASSES; ++p) {
       const int r = p * G::RPP + tid / G::CPR;
@@ -67,14 +77,39 @@ struct TileRegs {
   }
 };
 
+// Descriptor over the rows [0, N) of one (batch, head) slice of a [B, H, N, D] tensor.
+template <int D>
+__device__ __forceinline__ BufRsrc head_rsrc(const uint16_t* head_base, int64_t sn, int N) {
+  return make_rsrc(head_base, (uint32_t)(((int64_t)N - 1) * sn * 2 + D * 2));
+}
+
 // Sets to -inf the elements of a 32x32 accumulator (lane half g) whose row t0 + acc_row(i, g) lies
-// outside [lo, hi].
-__device__ __forceinline__ void mask_outside(f32x16_t& s, int lo, int hi, int t0, int g) {
-  const int a = lo - t0 - 4 * g, z = hi - t0 - 4 * g;
+// outside the lane's interval [lo, hi]. cut_lo / cut_hi (wave-uniform) tell whether the lower / upper
+// bound of some lane falls inside this block; usually only one does, so only one test runs.
+__device__ __forceinline__ void mask_cuts(f32x16_t& s, int lo, int hi, int t0, int g, bool cut_lo, bool cut_hi) {
+  if (cut_lo) {
+    const int a = lo - t0 - 4 * g;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int r = 8 * (i >> 2) + (i & 3);
-    s[i] = (r >= a && r <= z) ? s[i] : -INFINITY;
+    for (int i = 0; i < 16; ++i) s[i] = (8 * (i >> 2) + (i & 3) >= a) ? s[i] : -INFINITY;
+  }
+  if (cut_hi) {
+    const int z = hi - t0 - 4 * g;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = (8 * (i >> 2) + (i & 3) <= z) ? s[i] : -INFINITY;
+  }
+}
+
+// Masks a partial block: interval cuts, plus the per-pair id check of rows whose ids are arbitrary
+// (bits from qs_exact_bits / ks_exact_bits).
+template <bool EXACT, class BitsFn>
+__device__ __forceinline__ void mask_partial(f32x16_t& s, const Interval& r, const WaveSpan& w, int t0, int g,
+                                             BitsFn exact_bits) {
+  if constexpr (EXACT) {
+    mask_cuts(s, r.lo, r.hi, t0, g, t0 < w.max_lo, t0 + kBlock - 1 > w.min_hi);
+  } else {
+    const uint32_t bits = exact_bits();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = ((bits >> e) & 1u) ? s[e] : -INFINITY;
   }
 }
 
@@ -218,9 +253,96 @@ __device__ __forceinline__ void k_workgroup(const AttnArgs& a, int& b, int& h, i
   kt = k_tile_of(a, b, rank);
 }
 
-// Interval bits (rows of the accumulator inside [lo, hi]) for a block starting at t0.
-__device__ __forceinline__ uint32_t interval_keep_bits(int lo, int hi, int t0, int g) {
-  return interval_bits(lo, hi, t0, g);
+
+// Per-wave classes of the first 128 blocks of a loop as bitmasks (bit i: block i is not SKIP / is
+// FULL for this wave), built once, so the loops test two bits per pair of blocks instead of
+// re-deriving streams, spans and classes. Blocks from 128 on are classified on the fly.
+struct BlockMask {
+  uint64_t act0, act1, full0, full1;  // blocks 0..63 and 64..127 (separate words: no dynamic indexing)
+};
+
+template <class ClassFn>
+__device__ __forceinline__ BlockMask build_block_mask(int nb, ClassFn cls_of) {
+  BlockMask bm = {0ull, 0ull, 0ull, 0ull};
+  const int n = imin(nb, 128);
+  for (int i = 0; i < n; ++i) {
+    const int c = cls_of(i);
+    const uint64_t bit = 1ull << (i & 63);
+    const uint64_t a = c != TILE_SKIP ? bit : 0ull, f = c == TILE_FULL ? bit : 0ull;
+    if (i < 64) {
+      bm.act0 |= a;
+      bm.full0 |= f;
+    } else {
+      bm.act1 |= a;
+      bm.full1 |= f;
+    }
+  }
+  return bm;
+}
+
+// Two-bit activity and fullness codes of blocks i, i + 1 (i even; blocks >= nb are SKIP).
+template <class ClassFn>
+__device__ __forceinline__ void pair_codes(const BlockMask& bm, int i, int nb, ClassFn cls_of, int& act2, int& full2) {
+  if (i < 128) {
+    const int sh = i & 63;
+    act2 = (int)(((i < 64 ? bm.act0 : bm.act1) >> sh) & 3ull);
+    full2 = (int)(((i < 64 ? bm.full0 : bm.full1) >> sh) & 3ull);
+  } else {
+    act2 = full2 = 0;
+#pragma unroll
+    for (int y = 0; y < 2; ++y) {
+      const int c = i + y < nb ? cls_of(i + y) : TILE_SKIP;
+      act2 |= (c != TILE_SKIP) << y;
+      full2 |= (c == TILE_FULL) << y;
+    }
+  }
+}
+
+// Software pipeline over `nb` blocks taken in pairs (64 stream rows per iteration, one barrier per
+// pair). issue(j, slot) starts the global loads of pair j into register slot `slot` (of L),
+// put(slot, buf) writes a slot to LDS buffer `buf` (0/1), body(j, buf) computes pair j from LDS
+// buffer `buf`. Pair j + 1 + L is loaded while pair j is computed and reaches LDS L iterations
+// later, so each pair's loads have L full iterations to land. Unrolled by two, so slots and
+// buffers are compile-time indices.
+template <int L, class Issue, class Put, class Body>
+__device__ __forceinline__ void run_pairs(int nb, Issue&& issue, Put&& put, Body&& body) {
+  static_assert(L == 1 || L == 2, "lookahead of one or two pairs");
+  const int np = (nb + 1) >> 1;
+  if (np > 0) {
+    issue(0, 0);
+    put(0, 0);
+  }
+  vmem_wait_all();  // everything loaded before the loop is in registers
+#pragma unroll
+  for (int k = 1; k <= L; ++k)
+    if (k < np) issue(k, k % L);
+  __syncthreads();
+  for (int j0 = 0; j0 < np; j0 += 2) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = j0 + u;
+      if (j < np) {
+        if (j + 1 < np) put((u + 1) % L, u ^ 1);
+        if (j + 1 + L < np) issue(j + 1 + L, (u + 1) % L);
+        body(j, u);
+        __syncthreads();
+      }
+    }
+  }
+}
+
+// Maximum of the 32 elements of two accumulators as a shallow tree of 3-input maxima (the loops
+// are latency-bound, so the reduction depth matters more than its instruction count).
+__device__ __forceinline__ float max32(const f32x16_t& s, const f32x16_t& t) {
+  float m[11];
+#pragma unroll
+  for (int k = 0; k < 5; ++k) m[k] = fmaxf(fmaxf(s[3 * k], s[3 * k + 1]), s[3 * k + 2]);
+#pragma unroll
+  for (int k = 0; k < 5; ++k) m[5 + k] = fmaxf(fmaxf(t[3 * k], t[3 * k + 1]), t[3 * k + 2]);
+  m[10] = fmaxf(s[15], t[15]);
+  const float x = fmaxf(fmaxf(m[0], m[1]), m[2]), y = fmaxf(fmaxf(m[3], m[4]), m[5]);
+  const float z = fmaxf(fmaxf(m[6], m[7]), m[8]), w = fmaxf(m[9], m[10]);
+  return fmaxf(fmaxf(x, y), fmaxf(z, w));
 }
 
 }  // namespace sps

@@ -35,7 +35,9 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int check_tensor(const char* name, const void* p, const int64_t* st, int need) {
+// The kernels read each (batch, head) slice through a 32-bit buffer descriptor, so the byte span of
+// its N rows must stay below 2^31.
+int check_tensor(const char* name, const void* p, const int64_t* st, int need, int N, int D) {
   if (!need) return SPS_OK;
   if (!p) return fail(SPS_E_INVALID, "%s: null pointer", name);
   if (!st) return fail(SPS_E_INVALID, "%s: null strides", name);
@@ -44,6 +46,10 @@ int check_tensor(const char* name, const void* p, const int64_t* st, int need) {
     if (st[i] % 8 != 0)
       return fail(SPS_E_INVALID, "%s: stride %d (%lld) must be a multiple of 8 elements", name, i,
                   (long long)st[i]);
+  if (st[2] < 0) return fail(SPS_E_INVALID, "%s: negative sequence stride", name);
+  if (((int64_t)N - 1) * st[2] * 2 + (int64_t)D * 2 > INT32_MAX)
+    return fail(SPS_E_UNSUPPORTED, "%s: one head's rows span more than 2 GiB (N=%d, stride %lld)", name, N,
+                (long long)st[2]);
   return SPS_OK;
 }
 
@@ -163,8 +169,8 @@ int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype, const void* 
     return fail(SPS_E_UNSUPPORTED, "attention dtype code %d not supported (bf16, f16)", dtype);
   if ((rc = check_scale(sm_scale))) return rc;
   const int need = (int64_t)B * H * N > 0;
-  if ((rc = check_tensor("q", q, q_strides, need)) || (rc = check_tensor("k", k, k_strides, need)) ||
-      (rc = check_tensor("v", v, v_strides, need)) || (rc = check_tensor("o", o, o_strides, need)))
+  if ((rc = check_tensor("q", q, q_strides, need, N, D)) || (rc = check_tensor("k", k, k_strides, need, N, D)) ||
+      (rc = check_tensor("v", v, v_strides, need, N, D)) || (rc = check_tensor("o", o, o_strides, need, N, D)))
     return rc;
   if (need && !lse) return fail(SPS_E_INVALID, "lse: null pointer");
   if (!need) return SPS_OK;
@@ -192,8 +198,10 @@ static int attn_bwd_impl(int passes, int family, int B, int H, int N, int D, int
                          int docs_dtype, int64_t docs_stride_b, float sm_scale, int window, int has_pkw, int pkw,
                          void* workspace, size_t workspace_bytes, void* stream) {
   g_last_error.clear();
-  if (passes < 1 || passes > (SPS_BWD_DQ | SPS_BWD_DKDV))
-    return fail(SPS_E_INVALID, "backward pass selector %d is not SPS_BWD_DQ, SPS_BWD_DKDV or both", passes);
+  if ((passes & (SPS_BWD_DQ | SPS_BWD_DKDV)) == 0 ||
+      (passes & ~(SPS_BWD_DQ | SPS_BWD_DKDV | SPS_BWD_REUSE_LAYOUT)) != 0)
+    return fail(SPS_E_INVALID, "backward pass selector %d is not SPS_BWD_DQ, SPS_BWD_DKDV or both (optionally "
+                "with SPS_BWD_REUSE_LAYOUT)", passes);
   sps::AttnArgs a;
   int rc = setup_common(a, family, B, H, N, docs, docs_dtype, docs_stride_b, window, has_pkw, pkw,
                         workspace, workspace_bytes, 1);
@@ -203,10 +211,10 @@ static int attn_bwd_impl(int passes, int family, int B, int H, int N, int D, int
     return fail(SPS_E_UNSUPPORTED, "attention dtype code %d not supported (bf16, f16)", dtype);
   if ((rc = check_scale(sm_scale))) return rc;
   const int need = (int64_t)B * H * N > 0;
-  if ((rc = check_tensor("q", q, q_strides, need)) || (rc = check_tensor("k", k, k_strides, need)) ||
-      (rc = check_tensor("v", v, v_strides, need)) || (rc = check_tensor("o", o, o_strides, need)) ||
-      (rc = check_tensor("dout", dout, dout_strides, need)) || (rc = check_tensor("dq", dq, dq_strides, need)) ||
-      (rc = check_tensor("dk", dk, dk_strides, need)) || (rc = check_tensor("dv", dv, dv_strides, need)))
+  if ((rc = check_tensor("q", q, q_strides, need, N, D)) || (rc = check_tensor("k", k, k_strides, need, N, D)) ||
+      (rc = check_tensor("v", v, v_strides, need, N, D)) || (rc = check_tensor("o", o, o_strides, need, N, D)) ||
+      (rc = check_tensor("dout", dout, dout_strides, need, N, D)) || (rc = check_tensor("dq", dq, dq_strides, need, N, D)) ||
+      (rc = check_tensor("dk", dk, dk_strides, need, N, D)) || (rc = check_tensor("dv", dv, dv_strides, need, N, D)))
     return rc;
   if (need && !lse) return fail(SPS_E_INVALID, "lse: null pointer");
   if (!need) return SPS_OK;
@@ -231,9 +239,11 @@ static int attn_bwd_impl(int passes, int family, int B, int H, int N, int D, int
   a.scale2 = sm_scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // The row layout is computed by the dQ pass and left in the workspace for the dK/dV pass.
-  if (docs && (passes & SPS_BWD_DQ) && (rc = hip_status(sps::launch_row_layout(a, s), "document prepass")))
+  if (docs && (passes & SPS_BWD_DQ) && !(passes & SPS_BWD_REUSE_LAYOUT) &&
+      (rc = hip_status(sps::launch_row_layout(a, s), "document prepass")))
     return rc;
-  return hip_status(sps::launch_attn_bwd(a, D, dtype == SPS_DTYPE_F16, passes, s), "attention backward");
+  return hip_status(sps::launch_attn_bwd(a, D, dtype == SPS_DTYPE_F16, passes & (SPS_BWD_DQ | SPS_BWD_DKDV), s),
+                    "attention backward");
 }
 
 }  // extern "C"
@@ -260,10 +270,6 @@ int sps_attn_bwd_pass(int pass, int family, int B, int H, int N, int D, int dtyp
                       const int64_t* dk_strides, void* dv, const int64_t* dv_strides, const void* docs,
                       int docs_dtype, int64_t docs_stride_b, float sm_scale, int window, int has_pkw, int pkw,
                       void* workspace, size_t workspace_bytes, void* stream) {
-  if (pass != SPS_BWD_DQ && pass != SPS_BWD_DKDV) {
-    g_last_error.clear();
-    return fail(SPS_E_INVALID, "pass must be SPS_BWD_DQ or SPS_BWD_DKDV (got %d)", pass);
-  }
   return attn_bwd_impl(pass, family, B, H, N, D, dtype, q, q_strides, k, k_strides, v, v_strides, o, o_strides,
                        dout, dout_strides, lse, dq, dq_strides, dk, dk_strides, dv, dv_strides, docs, docs_dtype,
                        docs_stride_b, sm_scale, window, has_pkw, pkw, workspace, workspace_bytes, stream);

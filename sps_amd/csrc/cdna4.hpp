@@ -132,6 +132,25 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
+// Raw buffer access: a descriptor over `bytes` bytes from `base`; loads at offsets >= bytes return
+// zeros (the hardware range check), so tiles that run past the end of a sequence need no clamping.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+
+// The base and size must be wave-uniform; they are moved to scalar registers explicitly, because a
+// descriptor the compiler cannot prove uniform is kept in VGPRs and every load through it becomes a
+// readfirstlane loop.
+__device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t x = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+  void* p = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ u32x4_t buf_load_b128(BufRsrc r, uint32_t offset) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+}
+
 // s_waitcnt vmcnt(0): waits for every outstanding vector-memory load of the wave. Placed before a
 // software-pipelined loop so the compiler's wait counting does not fall back to vmcnt(0) inside it
 // for registers loaded before the loop.

@@ -240,3 +240,24 @@ def test_reference_assertions_preserved():
         SA.sps_sliding_attention(q, q, q, 0.125, 3, documents_idx_BxT=torch.zeros(1, 28, dtype=torch.long, device="cuda"))
     with pytest.raises(AssertionError):
         SA.full_attention(q[..., :48], q[..., :48], q[..., :48], 0.125)
+
+
+@pytest.mark.parametrize("family", ["sps", "full"])
+def test_backward_reusing_forward_layout_is_identical(family):
+    # attention_forward(keep_layout=True) leaves the document layout in a backward-sized workspace;
+    # the backward that reuses it (SPS_BWD_REUSE_LAYOUT) matches the one that recomputes it bit for bit.
+    rng = np.random.default_rng(11)
+    b, h, n, d = 2, 3, 1000, 64
+    tokens = n if family == "full" else n // 2
+    docs = torch.tensor(_packed_docs(rng, b, tokens, family, max_len=300), device="cuda")
+    g = torch.Generator().manual_seed(4)
+    q, k, v, do = (torch.randn((b, h, n, d), generator=g).to(torch.bfloat16).cuda() for _ in range(4))
+    fam = FAMILY[family]
+    o, lse, _, _, _, ws = SA.attention_forward(q, k, v, 0.125, fam, 17, docs, keep_layout=True)
+    assert ws is not None
+    ref = SA.attention_backward(do, q, k, v, o, lse, 0.125, fam, 17, docs)
+    got = SA.attention_backward(do, q, k, v, o, lse, 0.125, fam, 17, docs, layout_workspace=ws)
+    split = SA.attention_backward(do, q, k, v, o, lse, 0.125, fam, 17, docs, layout_workspace=ws,
+                                  between_passes=lambda: None)
+    for r, x, y in zip(ref, got, split):
+        assert torch.equal(r, x) and torch.equal(r, y)

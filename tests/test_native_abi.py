@@ -100,3 +100,14 @@ def test_last_error_truncates():
     buf = C.create_string_buffer(8)
     full = N.lib().sps_last_error(buf, len(buf))
     assert full > 7 and len(buf.value) == 7
+
+
+def test_backward_pass_selector_validation():
+    lib = N.lib()
+    st = N.i64_array((64 * 64, 64 * 64, 64))
+    p = 0x10000
+    for bad in (0, 4, 8, 16 | 1):
+        rc = lib.sps_attn_bwd_pass(bad, 1, 1, 1, 64, 64, N.DTYPE_BF16, p, st, p, st, p, st, p, st, p, st, 0x20000,
+                                   p, st, p, st, p, st, None, N.DTYPE_I64, 0, 0.125, 4, 0, -1, None, 0, None)
+        assert rc == N.SPS_E_INVALID, bad
+        assert "pass selector" in N.last_error()
