@@ -191,13 +191,12 @@ def bench_decode(cfg, steps: int, warmup: int):
             DA.KVSegment(ret[0].to(dev), ret[1].to(dev), ret[2].to(dev), max_len_cap=cfg.storage)]
     qd = q.to(dev)
     ex = [(a.to(dev), b.to(dev)) for a, b in extras]
-    # Kernel-level call: the inputs as sps_decode takes them (fp32 query and extras).
-    q32 = qd.float().view(cfg.seqs, 1, cfg.heads, cfg.head_dim).contiguous()
-    ex32 = [(a.float().contiguous(), b.float().contiguous()) for a, b in ex]
+    # Kernel-level call: the inputs as sps_decode takes them (bf16 query and extras, no casts).
+    q4 = qd.view(cfg.seqs, 1, cfg.heads, cfg.head_dim)
     out = torch.empty((cfg.seqs, 1, cfg.heads, cfg.head_dim), device=dev, dtype=torch.float32)
 
     def kernel_call():
-        DA._run_decode(q32, 1, segs, ex32, [1, 1], out)
+        DA._run_decode(q4, 1, segs, ex, [1, 1], out)
 
     def api_call():
         DA.masked_kv_attention(qd, segs, extra_kv=ex, attn_dtype=torch.bfloat16, prefer_triton=True)

@@ -155,24 +155,25 @@ size_t sps_decode_workspace_bytes(int B, int H, int D, int nq, int kv_dtype, int
 
 /*
  * Segmented decode attention, nq in {1, 2} queries per (batch, head).
- * q: fp32 [B, nq, H, D] (values already rounded to the attention dtype), strides {b, slot, h}.
+ * q: [B, nq, H, D] of q_dtype (SPS_DTYPE_BF16, F16 or F32; values already in the attention dtype),
+ * strides {b, slot, h}.
  * Segments (n_seg <= 3): K and V [B, H, storage, D] of kv_dtype (bf16, f16 or f32) with strides
  * {b, h, t}; live lengths seg_len[s] ([B] if seg_len_per_head[s] == 0, else [B, H]) of dtype
  * SPS_DTYPE_I32 or SPS_DTYPE_I64; key t of segment s is attended iff
  * t < min(max(len, 0), seg_scan[s]).
- * Extras (n_extra <= 2): fp32 [B, H, D] keys/values sharing strides {b, h}; extra e is attended by
- * query slot j iff bit j of extra_query_mask[e] is set (q=1: 1; q=2: current input 3, current
- * <predict> 2). out: fp32 [B, nq, H, D], strides {b, slot, h}; 0 where nothing is attended.
- * D in {16, 32, 64, 128, 256}.
+ * Extras (n_extra <= 2): [B, H, D] keys/values of extra_dtype sharing strides {b, h}; extra e is
+ * attended by query slot j iff bit j of extra_query_mask[e] is set (q=1: 1; q=2: current input 3,
+ * current <predict> 2). out: fp32 [B, nq, H, D], strides {b, slot, h}; 0 where nothing is attended.
+ * D in {16, 32, 64, 128, 256}. Two launches: per-chunk partials into the workspace, then a merge.
  */
 int sps_decode(int B, int H, int D, int nq,
-               const float* q, const int64_t* q_strides,
+               const void* q, int q_dtype, const int64_t* q_strides,
                int kv_dtype, int n_seg,
                const void* const* seg_k, const int64_t* seg_k_strides,
                const void* const* seg_v, const int64_t* seg_v_strides,
                const void* const* seg_len, const int* seg_len_dtype, const int* seg_len_per_head,
                const int64_t* seg_scan,
-               int n_extra, const float* const* extra_k, const float* const* extra_v,
+               int n_extra, const void* const* extra_k, const void* const* extra_v, int extra_dtype,
                const int64_t* extra_strides, const int* extra_query_mask,
                float sm_scale, float* out, const int64_t* out_strides,
                void* workspace, size_t workspace_bytes, void* stream);

@@ -91,9 +91,9 @@ _SIGNATURES = {
     "sps_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _pi64]),
     "sps_decode": (
         _i32,
-        [_i32, _i32, _i32, _i32, _p, _pi64, _i32, _i32]
+        [_i32, _i32, _i32, _i32, _p, _i32, _pi64, _i32, _i32]
         + [C.POINTER(_p), _pi64, C.POINTER(_p), _pi64, C.POINTER(_p), _pi32, _pi32, _pi64]
-        + [_i32, C.POINTER(_p), C.POINTER(_p), _pi64, _pi32]
+        + [_i32, C.POINTER(_p), C.POINTER(_p), _i32, _pi64, _pi32]
         + [_f32, _p, _pi64, _p, _sz, _p],
     ),
 }

@@ -305,19 +305,23 @@ size_t sps_decode_workspace_bytes(int B, int H, int D, int nq, int kv_dtype, int
   return align_up(bytes);
 }
 
-int sps_decode(int B, int H, int D, int nq, const float* q, const int64_t* q_strides, int kv_dtype, int n_seg,
-               const void* const* seg_k, const int64_t* seg_k_strides, const void* const* seg_v,
+int sps_decode(int B, int H, int D, int nq, const void* q, int q_dtype, const int64_t* q_strides, int kv_dtype,
+               int n_seg, const void* const* seg_k, const int64_t* seg_k_strides, const void* const* seg_v,
                const int64_t* seg_v_strides, const void* const* seg_len, const int* seg_len_dtype,
-               const int* seg_len_per_head, const int64_t* seg_scan, int n_extra, const float* const* extra_k,
-               const float* const* extra_v, const int64_t* extra_strides, const int* extra_query_mask,
-               float sm_scale, float* out, const int64_t* out_strides, void* workspace, size_t workspace_bytes,
-               void* stream) {
+               const int* seg_len_per_head, const int64_t* seg_scan, int n_extra, const void* const* extra_k,
+               const void* const* extra_v, int extra_dtype, const int64_t* extra_strides,
+               const int* extra_query_mask, float sm_scale, float* out, const int64_t* out_strides,
+               void* workspace, size_t workspace_bytes, void* stream) {
   g_last_error.clear();
   if (B < 0 || H < 0) return fail(SPS_E_INVALID, "negative size B=%d H=%d", B, H);
   if (nq != 1 && nq != 2) return fail(SPS_E_INVALID, "nq must be 1 or 2 (got %d)", nq);
   if (!decode_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "decode head_dim %d not supported", D);
   if (kv_dtype != SPS_DTYPE_BF16 && kv_dtype != SPS_DTYPE_F16 && kv_dtype != SPS_DTYPE_F32)
     return fail(SPS_E_UNSUPPORTED, "K/V dtype code %d not supported", kv_dtype);
+  if (q_dtype != SPS_DTYPE_BF16 && q_dtype != SPS_DTYPE_F16 && q_dtype != SPS_DTYPE_F32)
+    return fail(SPS_E_UNSUPPORTED, "query dtype code %d not supported", q_dtype);
+  if (n_extra > 0 && extra_dtype != SPS_DTYPE_BF16 && extra_dtype != SPS_DTYPE_F16 && extra_dtype != SPS_DTYPE_F32)
+    return fail(SPS_E_UNSUPPORTED, "extra K/V dtype code %d not supported", extra_dtype);
   if (n_seg < 0 || n_seg > sps::kMaxDecodeSegs)
     return fail(SPS_E_INVALID, "at most %d segments (got %d)", sps::kMaxDecodeSegs, n_seg);
   if (n_extra < 0 || n_extra > sps::kMaxDecodeExtras)
@@ -386,6 +390,8 @@ int sps_decode(int B, int H, int D, int nq, const float* q, const int64_t* q_str
     a.e_sb = extra_strides[0];
     a.e_sh = extra_strides[1];
   }
+  a.e_dtype = extra_dtype;
+  a.q_dtype = q_dtype;
   a.q = q;
   a.q_sb = q_strides[0];
   a.q_ss = q_strides[1];

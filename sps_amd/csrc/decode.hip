@@ -13,7 +13,9 @@
 // (all loads issued before any arithmetic), computes fp32 dot products with a short lane
 // reduction, and keeps an exp2-domain partial softmax; the four waves merge in LDS and the
 // workgroup writes one (acc[D], m, l) partial. Only live keys are read: chunks past the live
-// length exit before touching K/V. A second small kernel merges the partials with the extras.
+// length exit before touching K/V. A second small kernel merges the partials with the extras: one
+// wave per (sequence, head, query slot), lanes over chunks for the max and the sums, then batched
+// coalesced reads of the accumulators (no chain of dependent loads per chunk).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -53,6 +55,8 @@ __device__ __forceinline__ void unpack16(const u32x4_t w, float* out) {
     }
   }
 }
+
+__device__ __forceinline__ int imin_d(int x, int y) { return x < y ? x : y; }
 
 __device__ __forceinline__ int seg_live_len(const DecodeSeg& sg, int b, int h, int H) {
   if (sg.scan == 0) return 0;
@@ -112,9 +116,9 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const DecodeArgs a)
   float qv[NQ][EPL];
 #pragma unroll
   for (int qi = 0; qi < NQ; ++qi) {
-    const float* qrow = a.q + b * a.q_sb + qi * a.q_ss + h * a.q_sh + cc * EPL;
+    const int64_t q0 = b * a.q_sb + qi * a.q_ss + h * a.q_sh + cc * EPL;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) qv[qi][e] = qrow[e];
+    for (int e = 0; e < EPL; ++e) qv[qi][e] = load_as_f32(a.q, q0 + e, a.q_dtype);
   }
 
   using raw_t = typename KV::raw;
@@ -212,75 +216,117 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const DecodeArgs a)
   }
 }
 
-// One wave per (head, batch): merges the chunk partials and the extra keys, normalises, writes fp32.
+// Index of the k-th live chunk of (b, h) over the segments in order (chunks of segment s are
+// chunk_base[s] .. chunk_base[s] + nc[s] - 1).
+__device__ __forceinline__ int live_chunk(const DecodeArgs& a, const int* nc, int k) {
+  for (int s = 0; s < a.n_seg; ++s) {
+    if (k < nc[s]) return a.seg[s].chunk_base + k;
+    k -= nc[s];
+  }
+  return -1;
+}
+
+template <int N>
+__device__ __forceinline__ float wave_max_f(float x) {
+#pragma unroll
+  for (int o = 1; o < N; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+// One wave per (query slot, head, batch): merges the chunk partials and the extra keys, normalises
+// and writes fp32. Lanes own chunks for the max / sum reductions (in rounds of 64 chunks); the
+// accumulator pass reads 8 chunk records per batch, lanes over d, so loads are issued together.
 template <int D, int NQ>
 __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
   constexpr int DPL = (D + 63) / 64;  // output elements per lane
   constexpr int REC = DecodeGeom<D, 2>::REC;
-  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  int live[3];
-  for (int s = 0; s < a.n_seg; ++s) live[s] = seg_live_len(a.seg[s], b, h, a.H);
-  const float* part = a.part + ((int64_t)(b * a.H + h) * a.n_chunks) * NQ * REC;
+  const int qi = blockIdx.x, h = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+  int nc[kMaxDecodeSegs] = {0, 0, 0};
+  int total = 0;
+  for (int s = 0; s < a.n_seg; ++s) {
+    nc[s] = (seg_live_len(a.seg[s], b, h, a.H) + a.chunk_keys - 1) / a.chunk_keys;
+    total += nc[s];
+  }
+  const float* part = a.part + ((int64_t)(b * a.H + h) * a.n_chunks) * NQ * REC + qi * REC;
 
-  for (int qi = 0; qi < NQ; ++qi) {
-    const float* qrow = a.q + b * a.q_sb + qi * a.q_ss + h * a.q_sh;
-    float es[2];
-    bool eon[2];
-    for (int e = 0; e < a.n_extra; ++e) {
-      eon[e] = (a.emask[e] >> qi) & 1;
-      float d = 0.f;
-      const float* kr = a.ek[e] + b * a.e_sb + h * a.e_sh;
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) {
-        const int dd = lane + 64 * i;
-        if (dd < D) d = fmaf(qrow[dd], kr[dd], d);
-      }
-      d = xor_sum<64>(d);
-      es[e] = d * a.scale2;
-    }
-    float M = -INFINITY;
-    for (int s = 0; s < a.n_seg; ++s) {
-      const int nc = (live[s] + a.chunk_keys - 1) / a.chunk_keys;
-      for (int c = a.seg[s].chunk_base; c < a.seg[s].chunk_base + nc; ++c)
-        M = fmaxf(M, part[(c * NQ + qi) * REC + D]);
-    }
-    for (int e = 0; e < a.n_extra; ++e)
-      if (eon[e]) M = fmaxf(M, es[e]);
-    const float mu = M == -INFINITY ? 0.f : M;
-    float L = 0.f, A[DPL];
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) A[i] = 0.f;
-    for (int s = 0; s < a.n_seg; ++s) {
-      const int nc = (live[s] + a.chunk_keys - 1) / a.chunk_keys;
-      for (int c = a.seg[s].chunk_base; c < a.seg[s].chunk_base + nc; ++c) {
-        const float* rec = part + (c * NQ + qi) * REC;
-        const float f = fast_exp2(rec[D] - mu);
-        L = fmaf(f, rec[D + 1], L);
-#pragma unroll
-        for (int i = 0; i < DPL; ++i) {
-          const int dd = lane + 64 * i;
-          if (dd < D) A[i] = fmaf(f, rec[dd], A[i]);
-        }
-      }
-    }
-    for (int e = 0; e < a.n_extra; ++e) {
-      if (!eon[e]) continue;
-      const float f = fast_exp2(es[e] - mu);
-      L += f;
-      const float* vr = a.ev[e] + b * a.e_sb + h * a.e_sh;
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) {
-        const int dd = lane + 64 * i;
-        if (dd < D) A[i] = fmaf(f, vr[dd], A[i]);
-      }
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    float* orow = a.out + b * a.o_sb + qi * a.o_ss + h * a.o_sh;
+  // Extra keys: scores (all lanes hold them after the reduction).
+  const int64_t q0 = b * a.q_sb + qi * a.q_ss + h * a.q_sh;
+  float es[kMaxDecodeExtras] = {-INFINITY, -INFINITY};
+  for (int e = 0; e < a.n_extra; ++e) {
+    const int64_t e0 = b * a.e_sb + h * a.e_sh;
+    float d = 0.f;
 #pragma unroll
     for (int i = 0; i < DPL; ++i) {
       const int dd = lane + 64 * i;
-      if (dd < D) orow[dd] = A[i] * inv;
+      if (dd < D) d = fmaf(load_as_f32(a.q, q0 + dd, a.q_dtype), load_as_f32(a.ek[e], e0 + dd, a.e_dtype), d);
     }
+    d = xor_sum<64>(d);
+    if ((a.emask[e] >> qi) & 1) es[e] = d * a.scale2;
+  }
+
+  // Max over chunk maxima and extra scores.
+  float M = fmaxf(es[0], es[1]);
+  for (int k0 = 0; k0 < total; k0 += 64) {
+    const int c = k0 + lane < total ? live_chunk(a, nc, k0 + lane) : -1;
+    const float mc = part[(int64_t)(c < 0 ? 0 : c) * NQ * REC + D];  // in-bounds even for idle lanes
+    M = fmaxf(M, c >= 0 ? mc : -INFINITY);
+  }
+  M = wave_max_f<64>(M);
+  const float mu = M == -INFINITY ? 0.f : M;
+
+  // Sum of weights and the weighted accumulators.
+  float L = 0.f, A[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) A[i] = 0.f;
+  for (int k0 = 0; k0 < total; k0 += 64) {
+    const int c = k0 + lane < total ? live_chunk(a, nc, k0 + lane) : -1;
+    const float* rec = part + (int64_t)(c < 0 ? 0 : c) * NQ * REC;
+    const float mrec = rec[D], lrec = rec[D + 1];  // chunk 0's record for idle lanes: in bounds
+    const float f = c >= 0 ? fast_exp2(mrec - mu) : 0.f;
+    L += c >= 0 ? f * lrec : 0.f;
+    const int nk = imin_d(64, total - k0);
+    for (int j0 = 0; j0 < nk; j0 += 8) {
+      float fj[8];
+      const float* rj[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = imin_d(j0 + u, nk - 1);
+        fj[u] = j0 + u < nk ? __shfl(f, j) : 0.f;
+        const int cj = __shfl(c, j);
+        rj[u] = part + (int64_t)cj * NQ * REC;
+      }
+      float x[8][DPL];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) {
+          const int dd = lane + 64 * i;
+          x[u][i] = dd < D ? rj[u][dd] : 0.f;
+        }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) A[i] = fmaf(fj[u], x[u][i], A[i]);
+    }
+  }
+  L = xor_sum<64>(L);
+  for (int e = 0; e < a.n_extra; ++e) {
+    if (es[e] == -INFINITY) continue;
+    const float f = fast_exp2(es[e] - mu);
+    L += f;
+    const int64_t e0 = b * a.e_sb + h * a.e_sh;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+      const int dd = lane + 64 * i;
+      if (dd < D) A[i] = fmaf(f, load_as_f32(a.ev[e], e0 + dd, a.e_dtype), A[i]);
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  float* orow = a.out + b * a.o_sb + qi * a.o_ss + h * a.o_sh;
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) {
+    const int dd = lane + 64 * i;
+    if (dd < D) orow[dd] = A[i] * inv;
   }
 }
 
@@ -293,7 +339,7 @@ static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((decode_merge_kernel<D, NQ>), dim3(a.H, a.B), dim3(64), 0, stream, a);
+  hipLaunchKernelGGL((decode_merge_kernel<D, NQ>), dim3(NQ, a.H, a.B), dim3(64), 0, stream, a);
   return hipGetLastError();
 }
 

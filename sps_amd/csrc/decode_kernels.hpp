@@ -39,10 +39,12 @@ struct DecodeSeg {
 struct DecodeArgs {
   int B, H, NQ, n_seg, n_extra;
   DecodeSeg seg[kMaxDecodeSegs];
-  const float* q;  // fp32 (already rounded to the attention dtype), strides (b, slot, h), d stride 1
+  const void* q;  // [B, nq, H, D] of q_dtype (values in the attention dtype), strides (b, slot, h)
+  int q_dtype;    // 0 bf16, 1 f16, 2 f32
   int64_t q_sb, q_ss, q_sh;
-  const float* ek[kMaxDecodeExtras];  // fp32 extra keys/values [B, H, D], strides (b, h)
-  const float* ev[kMaxDecodeExtras];
+  const void* ek[kMaxDecodeExtras];  // extra keys/values [B, H, D] of e_dtype, strides (b, h)
+  const void* ev[kMaxDecodeExtras];
+  int e_dtype;
   int64_t e_sb, e_sh;
   int emask[kMaxDecodeExtras];  // bit s: query slot s attends this extra
   float scale2;                 // sm_scale * log2(e)
@@ -52,6 +54,14 @@ struct DecodeArgs {
   float* out;  // fp32, strides (b, slot, h), d stride 1
   int64_t o_sb, o_ss, o_sh;
 };
+
+// Element i of a bf16 / f16 / f32 array as fp32.
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dtype) {
+  if (dtype == 2) return reinterpret_cast<const float*>(p)[i];
+  const uint16_t x = reinterpret_cast<const uint16_t*>(p)[i];
+  if (dtype == 1) return (float)__builtin_bit_cast(_Float16, x);
+  return __builtin_bit_cast(float, (uint32_t)x << 16);
+}
 
 hipError_t launch_decode(const DecodeArgs& a, int D, int kv_dtype, hipStream_t stream);
 

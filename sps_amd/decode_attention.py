@@ -62,9 +62,17 @@ def _len_dtype(lengths: Tensor) -> int:
     raise TypeError(f"segment lengths must be int32 or int64, got {lengths.dtype}")
 
 
-def _run_decode(q_f32: Tensor, nq: int, segments, extras, extra_masks, out: Tensor) -> Tensor:
-    """Calls sps_decode. q_f32: [B, nq, H, D] fp32; extras: list of (k, v) fp32 [B, H, D]."""
-    b, _, h, d = q_f32.shape
+def _as_attn(t: Tensor, attn_dtype: torch.dtype) -> Tensor:
+    """The tensor in the attention dtype (no copy when it already is, and its last dim is contiguous)."""
+    if t.dtype != attn_dtype:
+        t = t.to(attn_dtype)
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor) -> Tensor:
+    """Calls sps_decode. q: [B, nq, H, D] (bf16/f16/f32); extras: list of (k, v) [B, H, D] sharing one
+    dtype and one (b, h) stride pair."""
+    b, _, h, d = q.shape
     kv_dtype = N.DTYPE_BF16
     if segments:
         kv_dtype = _KV_DTYPES[segments[0].k.dtype]
@@ -73,7 +81,7 @@ def _run_decode(q_f32: Tensor, nq: int, segments, extras, extra_masks, out: Tens
     lib = N.lib()
     scan_arr = N.i64_array(scans)
     ws_bytes = lib.sps_decode_workspace_bytes(b, h, d, nq, kv_dtype, len(segments), scan_arr)
-    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q_f32.device)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
     k_strides, v_strides = [], []
     for s in segments:
         k_strides += [s.k.stride(0), s.k.stride(1), s.k.stride(2)]
@@ -81,20 +89,30 @@ def _run_decode(q_f32: Tensor, nq: int, segments, extras, extra_masks, out: Tens
     ek = [e[0] for e in extras]
     ev = [e[1] for e in extras]
     e_strides = (ek[0].stride(0), ek[0].stride(1)) if extras else (0, 0)
+    e_dtype = _KV_DTYPES[ek[0].dtype] if extras else N.DTYPE_F32
     status = lib.sps_decode(
         b, h, d, nq,
-        q_f32.data_ptr(), N.i64_array((q_f32.stride(0), q_f32.stride(1), q_f32.stride(2))),
+        q.data_ptr(), _KV_DTYPES[q.dtype], N.i64_array((q.stride(0), q.stride(1), q.stride(2))),
         kv_dtype, len(segments),
         N.ptr_array([s.k.data_ptr() for s in segments]), N.i64_array(k_strides),
         N.ptr_array([s.v.data_ptr() for s in segments]), N.i64_array(v_strides),
         N.ptr_array([ln.data_ptr() for ln in lens]), N.i32_array([_len_dtype(ln) for ln in lens]),
         N.i32_array([int(ln.dim() == 2) for ln in lens]), scan_arr,
-        len(extras), N.ptr_array([t.data_ptr() for t in ek]), N.ptr_array([t.data_ptr() for t in ev]),
+        len(extras), N.ptr_array([t.data_ptr() for t in ek]), N.ptr_array([t.data_ptr() for t in ev]), e_dtype,
         N.i64_array(e_strides), N.i32_array(extra_masks),
         1.0 / math.sqrt(d), out.data_ptr(), N.i64_array((out.stride(0), out.stride(1), out.stride(2))),
-        ws.data_ptr(), ws.numel(), torch.cuda.current_stream(q_f32.device).cuda_stream,
+        ws.data_ptr(), ws.numel(), torch.cuda.current_stream(q.device).cuda_stream,
     )
     N.check("sps_decode", status)
+    return out
+
+
+def _extras_in(extra_kv, attn_dtype, b, h, d):
+    """Extra (k, v) pairs in the attention dtype with one shared (b, h) stride pair."""
+    out = [(_as_attn(ek, attn_dtype).expand(b, h, d), _as_attn(ev, attn_dtype).expand(b, h, d))
+           for ek, ev in extra_kv]
+    if len({(k.stride(0), k.stride(1)) for pair in out for k in pair}) > 1:
+        out = [(k.contiguous(), v.contiguous()) for k, v in out]
     return out
 
 
@@ -151,16 +169,13 @@ def triton_segmented_q1_attention(
         return None
     if not _segments_compatible(segments, batch_size, n_head, head_dim, q_BxHxD.device):
         return None
-    extras = []
-    for ek, ev in extra_kv or []:
-        extras.append(
-            (ek.to(attn_dtype).float().contiguous().expand(batch_size, n_head, head_dim).contiguous(),
-             ev.to(attn_dtype).float().contiguous().expand(batch_size, n_head, head_dim).contiguous())
-        )
-    q32 = q_BxHxD.to(attn_dtype).float().contiguous().view(batch_size, 1, n_head, head_dim)
+    if attn_dtype not in _KV_DTYPES:
+        return None
+    extras = _extras_in(extra_kv or [], attn_dtype, batch_size, n_head, head_dim)
+    q4 = _as_attn(q_BxHxD, attn_dtype).unsqueeze(1)
     out = torch.empty((batch_size, n_head, head_dim), device=q_BxHxD.device, dtype=torch.float32)
     out4 = out.view(batch_size, 1, n_head, head_dim)
-    _run_decode(q32, 1, list(segments), extras, [1] * len(extras), out4)
+    _run_decode(q4, 1, list(segments), extras, [1] * len(extras), out4)
     return out
 
 
@@ -217,15 +232,13 @@ def triton_segmented_q2_attention(
     if not _segments_compatible(segments, batch_size, n_head, head_dim, q_Bx2xHxD.device):
         raise RuntimeError("sps_amd q2 attention: segments must share a bf16/f16/f32 dtype, int lengths "
                            "of shape [B] or [B, H] and 16-byte aligned rows")
-    extras = [
-        (current_normal_k_BxHxD.to(attn_dtype).float().contiguous(),
-         current_normal_v_BxHxD.to(attn_dtype).float().contiguous()),
-        (current_predict_k_BxHxD.to(attn_dtype).float().contiguous(),
-         current_predict_v_BxHxD.to(attn_dtype).float().contiguous()),
-    ]
-    q32 = q_Bx2xHxD.to(attn_dtype).float().contiguous()
+    if attn_dtype not in _KV_DTYPES:
+        raise RuntimeError(f"sps_amd q2 attention supports attn_dtype bf16, f16 or f32, got {attn_dtype}")
+    extras = _extras_in([(current_normal_k_BxHxD, current_normal_v_BxHxD),
+                         (current_predict_k_BxHxD, current_predict_v_BxHxD)], attn_dtype, batch_size, n_head, head_dim)
+    q = _as_attn(q_Bx2xHxD, attn_dtype)
     out = torch.empty((batch_size, 2, n_head, head_dim), device=q_Bx2xHxD.device, dtype=torch.float32)
-    return _run_decode(q32, 2, list(segments), extras, [0b11, 0b10], out)
+    return _run_decode(q, 2, list(segments), extras, [0b11, 0b10], out)
 
 
 def masked_kv_attention(

@@ -81,18 +81,18 @@ def test_workspace_sizes():
     assert dec >= 64 * 16 * (1 + 16) * (64 + 4) * 4
 
 
-def test_decode_argument_validation():
-    lib = N.lib()
+def _decode(nq=1, D=64, n_seg=0, q_dtype=N.DTYPE_BF16, extra_dtype=N.DTYPE_BF16, n_extra=0):
     z = N.i64_array([0, 0, 0])
-    rc = lib.sps_decode(1, 1, 64, 3, 0x1000, z, N.DTYPE_BF16, 0, None, z, None, z, None, None, None, z,
-                        0, None, None, z, None, 0.125, 0x2000, z, None, 0, None)
-    assert rc == N.SPS_E_INVALID and "nq" in N.last_error()
-    rc = lib.sps_decode(1, 1, 48, 1, 0x1000, z, N.DTYPE_BF16, 0, None, z, None, z, None, None, None, z,
-                        0, None, None, z, None, 0.125, 0x2000, z, None, 0, None)
-    assert rc == N.SPS_E_UNSUPPORTED
-    rc = lib.sps_decode(1, 1, 64, 1, 0x1000, z, N.DTYPE_BF16, 4, None, z, None, z, None, None, None, z,
-                        0, None, None, z, None, 0.125, 0x2000, z, None, 0, None)
-    assert rc == N.SPS_E_INVALID and "segments" in N.last_error()
+    return N.lib().sps_decode(1, 1, D, nq, 0x1000, q_dtype, z, N.DTYPE_BF16, n_seg, None, z, None, z, None, None,
+                              None, z, n_extra, None, None, extra_dtype, z, None, 0.125, 0x2000, z, None, 0, None)
+
+
+def test_decode_argument_validation():
+    assert _decode(nq=3) == N.SPS_E_INVALID and "nq" in N.last_error()
+    assert _decode(D=48) == N.SPS_E_UNSUPPORTED
+    assert _decode(n_seg=4) == N.SPS_E_INVALID and "segments" in N.last_error()
+    assert _decode(q_dtype=N.DTYPE_I32) == N.SPS_E_UNSUPPORTED and "query dtype" in N.last_error()
+    assert _decode(n_extra=1, extra_dtype=N.DTYPE_I64) == N.SPS_E_UNSUPPORTED and "extra" in N.last_error()
 
 
 def test_last_error_truncates():
