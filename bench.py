@@ -50,6 +50,45 @@ def cpu_model() -> str:
 
 
 # ----------------------------------------------------------------------------------------------
+# HBM traffic per launch (from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this script)
+# ----------------------------------------------------------------------------------------------
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_c3_c5.txt"
+
+
+def copy_probe(mib: int) -> None:
+    """A plain streaming kernel of known size (torch.neg over `mib` MiB of fp32: reads and writes
+    `mib` MiB once each) for calibrating the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def recorded_traffic() -> dict:
+    """Calibrated HBM bytes per launch of each kernel, as recorded in TRAFFIC_FILE (lines
+    `<kernel> fetch_bytes=<n> write_bytes=<n>`); empty when the file is absent."""
+    out = {}
+    try:
+        text = TRAFFIC_FILE.read_text()
+    except OSError:
+        return out
+    for line in text.splitlines():
+        parts = line.split()
+        if len(parts) != 3 or not parts[1].startswith("fetch_bytes=") or not parts[2].startswith("write_bytes="):
+            continue
+        try:
+            out[parts[0]] = int(parts[1].split("=", 1)[1]) + int(parts[2].split("=", 1)[1])
+        except ValueError:
+            continue
+    return out
+
+
+# ----------------------------------------------------------------------------------------------
 # Prefill / training: C3
 # ----------------------------------------------------------------------------------------------
 def bench_attention(cfg, steps: int, warmup: int):
@@ -119,7 +158,8 @@ def bench_attention(cfg, steps: int, warmup: int):
         "kernels": {name: {"ms": round(x["ms"], 4), "tflops": round(x["tflops"], 2), "frac": round(x["frac"], 4),
                            "algorithmic_gflop": round(x["flop"] / 1e9, 3)} for name, x in kernels.items()},
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(dk["tflops"], 2),
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dk["frac"], 4), "traffic": None},
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dk["frac"], 4),
+                     "traffic": recorded_traffic().get(dominant)},
     }
 
 
@@ -231,7 +271,10 @@ def bench_decode(cfg, steps: int, warmup: int):
         "algorithmic_bytes": nbytes,
         "roofline": {"kernel": "decode_partial_kernel + decode_merge_kernel", "bound": "hbm",
                      "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None},
+                     "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "traffic": (lambda t: t["decode_partial_kernel"] + t["decode_merge_kernel"]
+                                 if "decode_partial_kernel" in t and "decode_merge_kernel" in t else None)(
+                                     recorded_traffic())},
         "_api_wall_s": time.perf_counter() - t0,
     }
 
@@ -270,12 +313,14 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work per baseline leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run a plain streaming kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every (batch, head) and every "
-              "decode sequence is independent; see DESIGN.md for how it would shard). Run with --gpus 1.",
+              "decode sequence is independent, so sharding needs no exchange inside attention). Run with --gpus 1.",
               file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
@@ -291,6 +336,9 @@ def main() -> int:
     from sps_amd.workloads import C3, C5
 
     _native.lib()
+    if args.copy_probe_mib > 0:
+        log(f"copy probe: torch.neg over {args.copy_probe_mib} MiB fp32, 3 launches")
+        copy_probe(args.copy_probe_mib)
     log(f"C3 fwd+bwd: {args.warmup} warm-up + {args.steps} timed steps")
     att = bench_attention(C3, args.steps, args.warmup)
     log(f"C3: {att['value']:.1f} TFLOP/s, {att['ms_per_step']:.3f} ms/step, kernels {att['kernels']}")

@@ -194,11 +194,21 @@ __device__ __forceinline__ void q_setup(const AttnArgs& a, const RowView& row, i
   p.n1 = wave_uniform(hi1 >= lo1 ? hi1 / kBlock - p.b1 + 1 : 0);
 }
 
-// Workgroup -> (row, head, query tile): ranks of the per-row heaviest-first order are outermost, so
-// every (row, head) pair keeps the same XCD (dispatch is round-robin over XCDs by block index).
+// Workgroup -> (row, head, tile): ranks of the per-row heaviest-first order are outermost, and
+// within a rank the (row, head) slots rotate by one batch row (H slots) per rank. The hardware deals
+// consecutive workgroups round-robin to its XCDs and, inside an XCD, to its shader engines, and
+// dispatches in order: without the rotation each engine would always receive the same batch rows;
+// rows packed with different documents carry different work, and the engines holding the lighter
+// rows would drain and idle while the others still hold work only they may start (measured: ~8% of
+// the attention time at the benchmark shape). When H is a multiple of the XCD count the rotation
+// keeps every (row, head) on one XCD, so its K/V tiles stay in that XCD's L2.
+__device__ __forceinline__ int row_rotation(int j, int rank, int H, int BH) {
+  return (int)(((int64_t)j + (int64_t)rank * H) % BH);
+}
+
 __device__ __forceinline__ void q_workgroup(const AttnArgs& a, int& b, int& h, int& qt) {
   const int BH = a.B * a.H;
-  const int rank = blockIdx.x / BH, bh = blockIdx.x - rank * BH;
+  const int rank = blockIdx.x / BH, bh = row_rotation(blockIdx.x - rank * BH, rank, a.H, BH);
   b = bh / a.H;
   h = bh - b * a.H;
   qt = q_tile_of(a, b, rank);
@@ -247,7 +257,7 @@ __device__ __forceinline__ void k_setup(const AttnArgs& a, const RowView& row, i
 
 __device__ __forceinline__ void k_workgroup(const AttnArgs& a, int& b, int& h, int& kt) {
   const int BH = a.B * a.H;
-  const int rank = blockIdx.x / BH, bh = blockIdx.x - rank * BH;
+  const int rank = blockIdx.x / BH, bh = row_rotation(blockIdx.x - rank * BH, rank, a.H, BH);
   b = bh / a.H;
   h = bh - b * a.H;
   kt = k_tile_of(a, b, rank);
