@@ -126,9 +126,15 @@ def bench_attention(cfg, steps: int, warmup: int):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        step(True)
+        step(False)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # Per-kernel durations from as many further steps with HIP events recorded between the kernels
+    # (kept out of the timed steps: on this stack each event record between two kernels leaves the
+    # GPU idle for ~6 us, which a training step does not pay).
+    for _ in range(steps):
+        step(True)
+    torch.cuda.synchronize()
 
     fwd = [e[0].elapsed_time(e[1]) for e in ev]
     dq = [e[1].elapsed_time(e[2]) for e in ev]
@@ -241,19 +247,21 @@ def bench_decode(cfg, steps: int, warmup: int):
     def api_call():
         DA.masked_kv_attention(qd, segs, extra_kv=ex, attn_dtype=torch.bfloat16, prefer_triton=True)
 
-    def timed(fn):
+    def timed(fn, reps: int = 5):
+        """Mean µs per call of `steps` back-to-back calls between two HIP events, median of `reps`."""
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
-        evs = []
-        for _ in range(steps):
+        out = []
+        for _ in range(reps):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            fn()
+            for _ in range(steps):
+                fn()
             e1.record()
-            evs.append((e0, e1))
-        torch.cuda.synchronize()
-        return [a.elapsed_time(b) * 1e3 for a, b in evs]
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1) * 1e3 / steps)
+        return out
 
     k_us = timed(kernel_call)
     torch.cuda.synchronize()

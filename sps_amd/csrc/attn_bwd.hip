@@ -89,15 +89,22 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
     }
   }
 
+  // Byte offset of block i's first row: i * (bytes per block) + a per-stream constant (modulo 2^32).
+  const uint32_t k_blk = (uint32_t)(kBlock * step * a.sk.n * 2), v_blk = (uint32_t)(kBlock * step * a.sv.n * 2);
+  const int c0 = stream_pos(m, plan.stream0, kBlock * plan.b0);
+  const int c1 = m.family == FAMILY_FULL ? 0 : stream_pos(m, STREAM_TEMPORARY, kBlock * plan.b1) - kBlock * step * plan.n0;
+  const uint32_t k_c0 = (uint32_t)(c0 * a.sk.n * 2), k_c1 = (uint32_t)(c1 * a.sk.n * 2);
+  const uint32_t v_c0 = (uint32_t)(c0 * a.sv.n * 2), v_c1 = (uint32_t)(c1 * a.sv.n * 2);
+
   TileRegs<D> rk[kLook][2], rv[kLook][2];
   auto issue = [&](int j, int slot) {
 #pragma unroll
     for (int y = 0; y < 2; ++y) {
       const int i = 2 * j + y;
       if (i < nb) {
-        const int pos0 = stream_pos(m, plan.stream(i), plan.first(i));
-        rk[slot][y].load(k_src, (uint32_t)(pos0 * a.sk.n * 2), k_off, tid);
-        rv[slot][y].load(v_src, (uint32_t)(pos0 * a.sv.n * 2), v_off, tid);
+        const bool s0 = i < plan.n0;
+        rk[slot][y].load(k_src, (uint32_t)i * k_blk + (s0 ? k_c0 : k_c1), k_off, tid);
+        rv[slot][y].load(v_src, (uint32_t)i * v_blk + (s0 ? v_c0 : v_c1), v_off, tid);
       }
     }
   };
@@ -115,7 +122,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
 
   auto run = [&](auto exact_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
+    auto cls_of = [&](int i) {
+      return classify_block(i < plan.n0 ? st.w0 : st.w1, plan.first(i), EXACT);
+    };
+    const BlockMask bm = build_block_mask(nb, cls_of);
     run_pairs<kLook>(nb, issue, put, [&](int j, int buf) {
+      int act2, full2;
+      pair_codes(bm, 2 * j, nb, cls_of, act2, full2);
 #pragma unroll
       for (int y = 0; y < 2; ++y) {
         const int i = 2 * j + y;
@@ -123,8 +136,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
         const int t0 = plan.first(i);
         const WaveSpan ws = s0 ? st.w0 : st.w1;
         const Interval lr = s0 ? st.r0 : st.r1;
-        const int cls = i < nb ? classify_block(ws, t0, EXACT) : TILE_SKIP;
-        if (cls != TILE_SKIP) {
+        if ((act2 >> y) & 1) {
           const uint16_t* tK = sK[buf][y];
           const uint16_t* tV = sV[buf][y];
           f32x16_t sc = {}, dp = {};
@@ -133,7 +145,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
             sc = E::mfma(lds_read_b128(tK + c32 * G::RS + 16 * c + 8 * g), qf[c], sc);
             dp = E::mfma(lds_read_b128(tV + c32 * G::RS + 16 * c + 8 * g), dof[c], dp);
           }
-          if (cls == TILE_PARTIAL)
+          if (!((full2 >> y) & 1))
             mask_partial<EXACT>(sc, lr, ws, t0, g,
                                 [&] { return qs_exact_bits(a, b, lr, plan.stream(i), t0, g, dq_doc); });
           uint32_t dsk[8];
@@ -237,17 +249,21 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
     }
   }
 
+  // Byte offset of chunk i's first row: i * (bytes per chunk) + the first chunk's offset.
+  const uint32_t q_blk = (uint32_t)(kBlock * a.sq.n * 2), o_blk = (uint32_t)(kBlock * a.sdo.n * 2);
+  const uint32_t q_c0 = (uint32_t)((int64_t)st.c0 * kBlock * a.sq.n * 2);
+  const uint32_t o_c0 = (uint32_t)((int64_t)st.c0 * kBlock * a.sdo.n * 2);
+
   ChunkRegs<D> rc[kLook][2];
   auto issue = [&](int j, int slot) {
 #pragma unroll
     for (int y = 0; y < 2; ++y) {
       const int i = 2 * j + y;
       if (i < nc) {
-        const int q0 = (st.c0 + i) * kBlock;
-        rc[slot][y].q.load(q_src, (uint32_t)(q0 * a.sq.n * 2), q_off, tid);
-        rc[slot][y].o.load(o_src, (uint32_t)(q0 * a.sdo.n * 2), o_off, tid);
+        rc[slot][y].q.load(q_src, q_c0 + (uint32_t)i * q_blk, q_off, tid);
+        rc[slot][y].o.load(o_src, o_c0 + (uint32_t)i * o_blk, o_off, tid);
         if (tid < kBlock) {
-          const int qp = imin(q0 + tid, m.N - 1);
+          const int qp = imin((st.c0 + i) * kBlock + tid, m.N - 1);
           const float l = lse_row[qp];
           rc[slot][y].lse = l == -INFINITY ? 0.f : l;  // a query with no visible key: its scores are all masked
           rc[slot][y].delta = delta_row[qp];
@@ -276,13 +292,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
 
   auto run = [&](auto exact_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
+    auto cls_of = [&](int i) { return classify_block(st.w, (st.c0 + i) * kBlock, EXACT); };
+    const BlockMask bm = build_block_mask(nc, cls_of);
     run_pairs<kLook>(nc, issue, put, [&](int j, int buf) {
+      int act2, full2;
+      pair_codes(bm, 2 * j, nc, cls_of, act2, full2);
 #pragma unroll
       for (int y = 0; y < 2; ++y) {
         const int i = 2 * j + y;
         const int qc = (st.c0 + i) * kBlock;
-        const int cls = i < nc ? classify_block(st.w, qc, EXACT) : TILE_SKIP;
-        if (cls != TILE_SKIP) {
+        if ((act2 >> y) & 1) {
           const uint16_t* tQ = sQ[buf][y];
           const uint16_t* tDO = sDO[buf][y];
           f32x16_t sc = {}, dp = {};
@@ -291,7 +310,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
             sc = E::mfma(lds_read_b128(tQ + c32 * G::RS + 16 * c + 8 * g), kf[c], sc);
             dp = E::mfma(lds_read_b128(tDO + c32 * G::RS + 16 * c + 8 * g), vf[c], dp);
           }
-          if (cls == TILE_PARTIAL)
+          if (!((full2 >> y) & 1))
             mask_partial<EXACT>(sc, st.r, st.w, qc, g,
                                 [&] { return ks_exact_bits(a, b, kp, st.r.hi, qc, g, dk_doc); });
           uint32_t pk[8], dsk[8];

@@ -94,6 +94,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
         const bool s0 = i < plan.n0;
         rk[slot][y].load(k_src, (uint32_t)i * k_blk + (s0 ? k_c0 : k_c1), k_off, tid);
         rv[slot][y].load(v_src, (uint32_t)i * v_blk + (s0 ? v_c0 : v_c1), v_off, tid);
+      } else {
+        rk[slot][y].zero();
+        rv[slot][y].zero();
       }
     }
   };

@@ -67,6 +67,13 @@ struct TileRegs {
     }
   }
 
+  // A block past the end of the plan: zeros, so its LDS tile (computed on, then masked) holds finite
+  // values and contributes exactly 0 to the products.
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int p = 0; p < G::PASSES; ++p) v[p] = u32x4_t{0u, 0u, 0u, 0u};
+  }
+
   __device__ __forceinline__ void store(uint16_t* tile, int tid) const {
 #pragma unroll
     for (int p = 0; p < G::PASSES; ++p) {
