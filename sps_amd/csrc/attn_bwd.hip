@@ -264,8 +264,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
         rc[slot][y].o.load(o_src, o_c0 + (uint32_t)i * o_blk, o_off, tid);
         if (tid < kBlock) {
           const int qp = imin((st.c0 + i) * kBlock + tid, m.N - 1);
-          const float l = lse_row[qp];
-          rc[slot][y].lse = l == -INFINITY ? 0.f : l;  // a query with no visible key: its scores are all masked
+          // Raw values: anything computed from them here would wait for this pair's loads now
+          // instead of when the pair is written to LDS one iteration later.
+          rc[slot][y].lse = lse_row[qp];
           rc[slot][y].delta = delta_row[qp];
         }
       }
@@ -277,7 +278,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
       rc[slot][y].q.store(sQ[buf][y], tid);
       rc[slot][y].o.store(sDO[buf][y], tid);
       if (tid < kBlock) {
-        sLse[buf][y][tid] = rc[slot][y].lse;
+        const float l = rc[slot][y].lse;
+        sLse[buf][y][tid] = l == -INFINITY ? 0.f : l;  // a query with no visible key: its scores are all masked
         sDelta[buf][y][tid] = rc[slot][y].delta;
       }
     }
