@@ -267,6 +267,31 @@ def bench_decode(cfg, steps: int, warmup: int):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     a_us = timed(api_call)
+
+    # The layer's KV-cache update that follows the attention in the same decode step (ring insert of
+    # the current input K/V, retained append of the current <predict> K/V), on caches of the C5
+    # shape; lengths stay inside the storage, so every step does the full update.
+    from sps_amd.decode_attention_fast import fused_sps_kv_update
+
+    B, H, D = cfg.seqs, cfg.heads, cfg.head_dim
+    upd_ring_k = torch.zeros((B, H, cfg.ring, D), device=dev, dtype=torch.bfloat16)
+    upd_ring_v = torch.zeros_like(upd_ring_k)
+    upd_ret_k = torch.zeros((B, H, cfg.storage, D), device=dev, dtype=torch.bfloat16)
+    upd_ret_v = torch.zeros_like(upd_ret_k)
+    upd_ring_len = torch.zeros((B,), device=dev, dtype=torch.int64)
+    upd_ring_pos = torch.zeros((B,), device=dev, dtype=torch.int64)
+    upd_ret_len = torch.zeros((B, H), device=dev, dtype=torch.int64)
+    active = torch.ones((B,), device=dev, dtype=torch.bool)
+
+    def update_call():
+        fused_sps_kv_update(nw_k=upd_ring_k, nw_v=upd_ring_v, nw_len=upd_ring_len, nw_pos=upd_ring_pos,
+                            br_k=upd_ret_k, br_v=upd_ret_v, br_len=upd_ret_len, k_window_BxHxD=ex[0][0],
+                            v_window_BxHxD=ex[0][1], k_retained_BxHxD=ex[1][0], v_retained_BxHxD=ex[1][1],
+                            active_mask_B=active, window_tokens=cfg.ring)
+
+    u_us = timed(update_call, reps=3)
+    upd_ret_len.zero_()
+    upd_bytes = 8 * B * H * D * 2  # four [B, H, D] bf16 rows read and written once
     nbytes = decode_bytes(cfg, lengths, nq=1, n_extra=2, kv_bytes=2)
     k_med = statistics.median(k_us)
     gbps = nbytes / (k_med * 1e-6) / 1e9
@@ -275,6 +300,8 @@ def bench_decode(cfg, steps: int, warmup: int):
                     "ring 64, 1 <predict> query (ring + retained + current input + current <predict>)",
         "us_per_step": round(k_med, 3),
         "api_us_per_step": round(statistics.median(a_us), 3),
+        "kv_update_us": round(statistics.median(u_us), 3),
+        "kv_update_gbps": round(upd_bytes / (statistics.median(u_us) * 1e-6) / 1e9, 1),
         "gbps": round(gbps, 1),
         "algorithmic_bytes": nbytes,
         "roofline": {"kernel": "decode_partial_kernel + decode_merge_kernel", "bound": "hbm",

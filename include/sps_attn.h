@@ -23,6 +23,7 @@
  *                                    (attention/triton_full_flash_attention.py:463-676)
  *   sps_decode                    <- triton_segmented_q1_attention (utils/decode_attention.py:393-480),
  *                                    triton_segmented_q2_attention (utils/decode_attention.py:483-594)
+ *   sps_kv_update                 <- fused_sps_kv_update (utils/decode_attention_fast.py:139-221)
  *   sps_attn_mask                 <- the mask block of _attn_fwd_inner_sps
  *                                    (attention/triton_sps_flash_attention.py:70-111); a
  *                                    verification entry point that materialises the mask the
@@ -51,6 +52,7 @@ extern "C" {
 #define SPS_DTYPE_F32 2
 #define SPS_DTYPE_I32 3
 #define SPS_DTYPE_I64 4
+#define SPS_DTYPE_U8 5 /* bool / uint8 flags (nonzero = true) */
 
 /* Attention families (mask semantics). */
 #define SPS_FAMILY_FULL 0        /* causal + document mask (full_attention) */
@@ -177,6 +179,32 @@ int sps_decode(int B, int H, int D, int nq,
                const int64_t* extra_strides, const int* extra_query_mask,
                float sm_scale, float* out, const int64_t* out_strides,
                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Decode KV-cache update of one layer, one launch (replaces fused_sps_kv_update,
+ * utils/decode_attention_fast.py:139-221; semantics of the un-fused path it replaces,
+ * _update_normal_memory_unfused / _update_predict_memory_unfused, reverse_sps/inference.py:137-168
+ * and 240-268). For every sequence b with active[b * active_stride] != 0:
+ *   ring (window_tokens > 0): slot = ring_len[b] >= window_tokens ? ring_pos[b] : ring_len[b];
+ *     ring K/V[b, h, slot, :] = k_window / v_window[b, h, :] for every head; then ring_len[b] += 1
+ *     if the ring was not full, else ring_pos[b] = (ring_pos[b] + 1) % window_tokens.
+ *   retained: if 0 <= ret_len[b, h] < ret_storage: retained K/V[b, h, ret_len[b, h], :] =
+ *     k_retained / v_retained[b, h, :] and ret_len[b, h] += 1 (otherwise nothing is written).
+ * Inactive sequences are untouched. Caches: [B, H, storage, D] of kv_dtype (bf16, f16, f32) with
+ * element strides ring_strides = {k_b, k_h, k_t, v_b, v_h, v_t} (likewise ret_strides), D axis
+ * contiguous. ring_len / ring_pos: [B] with strides ring_len_strides = {len_b, pos_b}; ret_len:
+ * [B, H] with strides {b, h}; all of len_dtype (int32/int64). New K/V: [B, H, D] of new_dtype,
+ * strides new_strides = {kw_b, kw_h, vw_b, vw_h, kr_b, kr_h, vr_b, vr_h}, converted to kv_dtype
+ * with round-to-nearest-even. active: [B] of SPS_DTYPE_U8 (bool), I32 or I64. The ring pointers may
+ * be null when window_tokens <= 0. window_tokens must not exceed ring_storage.
+ */
+int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v, const int64_t* ring_strides,
+                  int ring_storage, int window_tokens, void* ring_len, void* ring_pos,
+                  const int64_t* ring_len_strides, void* ret_k, void* ret_v, const int64_t* ret_strides,
+                  int ret_storage, void* ret_len, const int64_t* ret_len_strides, int len_dtype, int new_dtype,
+                  const void* k_window, const void* v_window, const void* k_retained, const void* v_retained,
+                  const int64_t* new_strides, const void* active, int active_dtype, int64_t active_stride,
+                  void* stream);
 
 #ifdef __cplusplus
 }

@@ -18,5 +18,8 @@ Pinning (what makes each function trustworthy; see tests/test_oracle_*.py):
                            backward formulas), finite differences, softmax invariants.
   decode                 — the reference test's explicit per-(b,h) softmax semantics, dense SPS
                            attention == stepwise decode over ring + retained + current keys.
+  kv update              — the reference's ring-wrap KAT (delayed_state/test_forward_efficient.py),
+                           the closed form of a ring after n inserts (insert i in slot i mod W,
+                           len = min(n, W), pos = n mod W once full), retained append up to storage.
   document ids           — reference KATs (core/test_document_idx.py).
 """

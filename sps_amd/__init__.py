@@ -3,7 +3,7 @@
 Drop-in replacements for the reference's attention entry points:
   prefill / training: ``sps_sliding_attention``, ``reverse_sps_sliding_attention``, ``full_attention``
   decode:             ``KVSegment``, ``triton_segmented_q1_attention``, ``triton_segmented_q2_attention``,
-                      ``masked_kv_attention``
+                      ``masked_kv_attention``, ``fused_sps_kv_update`` (KV-cache update)
   document ids:       ``generate_left_padded_document_idx``
 All compute runs in libsps_attn.so (hand-written HIP kernels); see include/sps_attn.h.
 """
@@ -15,6 +15,7 @@ from .decode_attention import (
     triton_segmented_q1_attention,
     triton_segmented_q2_attention,
 )
+from .decode_attention_fast import fused_sps_kv_update
 from .document_idx import (
     compute_left_padded_position_ids,
     generate_left_padded_document_idx,
@@ -31,6 +32,7 @@ __all__ = [
     "triton_segmented_q1_attention",
     "triton_segmented_q2_attention",
     "masked_kv_attention",
+    "fused_sps_kv_update",
     "generate_left_padded_document_idx",
     "compute_left_padded_position_ids",
     "infer_is_real_tokens",

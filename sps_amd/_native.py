@@ -22,6 +22,7 @@ DTYPE_F16 = 1
 DTYPE_F32 = 2
 DTYPE_I32 = 3
 DTYPE_I64 = 4
+DTYPE_U8 = 5
 
 BWD_DQ = 1
 BWD_DKDV = 2
@@ -41,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "sps_attn_mask",
     "sps_decode_workspace_bytes",
     "sps_decode",
+    "sps_kv_update",
 )
 
 _i32 = C.c_int
@@ -95,6 +97,14 @@ _SIGNATURES = {
         + [C.POINTER(_p), _pi64, C.POINTER(_p), _pi64, C.POINTER(_p), _pi32, _pi32, _pi64]
         + [_i32, C.POINTER(_p), C.POINTER(_p), _i32, _pi64, _pi32]
         + [_f32, _p, _pi64, _p, _sz, _p],
+    ),
+    "sps_kv_update": (
+        _i32,
+        [_i32, _i32, _i32, _i32]
+        + [_p, _p, _pi64, _i32, _i32, _p, _p, _pi64]  # ring
+        + [_p, _p, _pi64, _i32, _p, _pi64, _i32]  # retained, length dtype
+        + [_i32, _p, _p, _p, _p, _pi64]  # new K/V
+        + [_p, _i32, _i64, _p],
     ),
 }
 

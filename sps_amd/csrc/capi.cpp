@@ -405,4 +405,100 @@ int sps_decode(int B, int H, int D, int nq, const void* q, int q_dtype, const in
   return hip_status(sps::launch_decode(a, D, kv_dtype, static_cast<hipStream_t>(stream)), "decode");
 }
 
+int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v, const int64_t* ring_strides,
+                  int ring_storage, int window_tokens, void* ring_len, void* ring_pos,
+                  const int64_t* ring_len_strides, void* ret_k, void* ret_v, const int64_t* ret_strides,
+                  int ret_storage, void* ret_len, const int64_t* ret_len_strides, int len_dtype, int new_dtype,
+                  const void* k_window, const void* v_window, const void* k_retained, const void* v_retained,
+                  const int64_t* new_strides, const void* active, int active_dtype, int64_t active_stride,
+                  void* stream) {
+  g_last_error.clear();
+  if (B < 0 || H < 0 || D < 0) return fail(SPS_E_INVALID, "negative size B=%d H=%d D=%d", B, H, D);
+  auto float_type = [](int t) { return t == SPS_DTYPE_BF16 || t == SPS_DTYPE_F16 || t == SPS_DTYPE_F32; };
+  if (!float_type(kv_dtype)) return fail(SPS_E_UNSUPPORTED, "cache dtype code %d not supported", kv_dtype);
+  if (!float_type(new_dtype)) return fail(SPS_E_UNSUPPORTED, "new K/V dtype code %d not supported", new_dtype);
+  if (len_dtype != SPS_DTYPE_I32 && len_dtype != SPS_DTYPE_I64)
+    return fail(SPS_E_INVALID, "lengths must be int32 or int64 (dtype code %d)", len_dtype);
+  int active_bytes = 0;
+  if (active_dtype == SPS_DTYPE_U8) active_bytes = 1;
+  else if (active_dtype == SPS_DTYPE_I32) active_bytes = 4;
+  else if (active_dtype == SPS_DTYPE_I64) active_bytes = 8;
+  else return fail(SPS_E_INVALID, "active mask must be bool/uint8, int32 or int64 (dtype code %d)", active_dtype);
+  if (ret_storage < 0 || ring_storage < 0) return fail(SPS_E_INVALID, "negative cache storage");
+  if ((int64_t)B * H * D == 0) return SPS_OK;
+  if (!active || !ret_k || !ret_v || !ret_len || !k_retained || !v_retained || !ret_strides || !ret_len_strides ||
+      !new_strides)
+    return fail(SPS_E_INVALID, "retained cache / new K/V / active mask: null pointer");
+  if (window_tokens > 0) {
+    if (!ring_k || !ring_v || !ring_len || !ring_pos || !k_window || !v_window || !ring_strides || !ring_len_strides)
+      return fail(SPS_E_INVALID, "ring cache: null pointer");
+    if (window_tokens > ring_storage)
+      return fail(SPS_E_INVALID, "window_tokens %d exceeds the ring storage %d", window_tokens, ring_storage);
+  }
+  sps::KvUpdateArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.B = B;
+  a.H = H;
+  a.D = D;
+  a.kv_dtype = kv_dtype;
+  a.new_dtype = new_dtype;
+  a.window = window_tokens > 0 ? window_tokens : 0;
+  if (a.window > 0) {
+    a.ring_k = ring_k;
+    a.ring_v = ring_v;
+    a.rk_sb = ring_strides[0];
+    a.rk_sh = ring_strides[1];
+    a.rk_st = ring_strides[2];
+    a.rv_sb = ring_strides[3];
+    a.rv_sh = ring_strides[4];
+    a.rv_st = ring_strides[5];
+    a.ring_storage = ring_storage;
+    a.ring_len = ring_len;
+    a.ring_pos = ring_pos;
+    a.ring_len_sb = ring_len_strides[0];
+    a.ring_pos_sb = ring_len_strides[1];
+    a.kw = k_window;
+    a.vw = v_window;
+    a.kw_sb = new_strides[0];
+    a.kw_sh = new_strides[1];
+    a.vw_sb = new_strides[2];
+    a.vw_sh = new_strides[3];
+  }
+  a.ret_k = ret_k;
+  a.ret_v = ret_v;
+  a.tk_sb = ret_strides[0];
+  a.tk_sh = ret_strides[1];
+  a.tk_st = ret_strides[2];
+  a.tv_sb = ret_strides[3];
+  a.tv_sh = ret_strides[4];
+  a.tv_st = ret_strides[5];
+  a.ret_storage = ret_storage;
+  a.ret_len = ret_len;
+  a.ret_len_sb = ret_len_strides[0];
+  a.ret_len_sh = ret_len_strides[1];
+  a.len_i64 = len_dtype == SPS_DTYPE_I64;
+  a.kr = k_retained;
+  a.vr = v_retained;
+  a.kr_sb = new_strides[4];
+  a.kr_sh = new_strides[5];
+  a.vr_sb = new_strides[6];
+  a.vr_sh = new_strides[7];
+  a.active = active;
+  a.active_bytes = active_bytes;
+  a.active_sb = active_stride;
+  // 16-byte pieces when no conversion is needed and every row start is 16-byte aligned.
+  const int64_t esz = kv_dtype == SPS_DTYPE_F32 ? 4 : 2;
+  bool vec = new_dtype == kv_dtype && (D * esz) % 16 == 0 && H <= sps::kMaxVecHeads;
+  const void* bases[] = {a.ret_k, a.ret_v, a.kr, a.vr, a.window > 0 ? a.ring_k : nullptr,
+                         a.window > 0 ? a.ring_v : nullptr, a.window > 0 ? a.kw : nullptr,
+                         a.window > 0 ? a.vw : nullptr};
+  for (const void* p : bases) vec = vec && aligned16(p);
+  const int64_t strides[] = {a.tk_sb, a.tk_sh, a.tk_st, a.tv_sb, a.tv_sh, a.tv_st, a.kr_sb, a.kr_sh, a.vr_sb,
+                             a.vr_sh, a.rk_sb, a.rk_sh, a.rk_st, a.rv_sb, a.rv_sh, a.rv_st, a.kw_sb, a.kw_sh,
+                             a.vw_sb, a.vw_sh};
+  for (int64_t st : strides) vec = vec && (st * esz) % 16 == 0;
+  a.vec16 = vec ? 1 : 0;
+  return hip_status(sps::launch_kv_update(a, static_cast<hipStream_t>(stream)), "kv update");
+}
+
 }  // extern "C"

@@ -65,4 +65,41 @@ __device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dtype
 
 hipError_t launch_decode(const DecodeArgs& a, int D, int kv_dtype, hipStream_t stream);
 
+// Decode KV-cache update of one layer: ring (normal window) insert + retained append.
+constexpr int kMaxVecHeads = 1024;  // heads per sequence the 16-byte path keeps in LDS
+
+struct KvUpdateArgs {
+  int B, H, D;
+  int kv_dtype;   // cache element type: 0 bf16, 1 f16, 2 f32
+  int new_dtype;  // new K/V element type (converted to kv_dtype, round to nearest even)
+  // Ring: K/V [B, H, storage, D] (strides b, h, t); len and pos [B]; window <= 0 leaves it untouched.
+  void* ring_k;
+  void* ring_v;
+  int64_t rk_sb, rk_sh, rk_st, rv_sb, rv_sh, rv_st;
+  int ring_storage, window;
+  void* ring_len;
+  void* ring_pos;
+  int64_t ring_len_sb, ring_pos_sb;
+  // Retained: K/V [B, H, storage, D]; len [B, H].
+  void* ret_k;
+  void* ret_v;
+  int64_t tk_sb, tk_sh, tk_st, tv_sb, tv_sh, tv_st;
+  int ret_storage;
+  void* ret_len;
+  int64_t ret_len_sb, ret_len_sh;
+  int len_i64;  // lengths and positions: int64 (else int32)
+  // New K/V [B, H, D] (strides b, h) for the ring slot and the retained slot.
+  const void* kw;
+  const void* vw;
+  const void* kr;
+  const void* vr;
+  int64_t kw_sb, kw_sh, vw_sb, vw_sh, kr_sb, kr_sh, vr_sb, vr_sh;
+  const void* active;  // [B]: nonzero = update this sequence
+  int active_bytes;    // 1, 4 or 8
+  int64_t active_sb;
+  int vec16;  // same dtype, rows and strides 16-byte aligned, H <= kMaxVecHeads: 16-byte pieces
+};
+
+hipError_t launch_kv_update(const KvUpdateArgs& a, hipStream_t stream);
+
 }  // namespace sps

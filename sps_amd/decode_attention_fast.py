@@ -1,0 +1,106 @@
+"""Decode KV-cache update of one layer in one launch (ring insert + retained append).
+
+Drop-in for the reference's ``fused_sps_kv_update`` (utils/decode_attention_fast.py:139-221): same
+keyword-only signature and shape asserts. Semantics follow the un-fused path it replaces,
+``_update_normal_memory_unfused`` / ``_update_predict_memory_unfused``
+(reverse_sps/inference.py:137-168, 240-268), with the fused kernel's retained bound check
+(decode_attention_fast.py:95-104): a retained buffer that is already full is left as it is.
+
+For every active sequence b:
+  ring (``window_tokens > 0``): slot = len[b] if the ring is not full, else pos[b]; every head's
+  K/V row at that slot is replaced; then len[b] += 1 while the ring fills, else
+  pos[b] = (pos[b] + 1) % window_tokens.
+  retained: if 0 <= len[b, h] < storage, K/V[b, h, len[b, h]] = new and len[b, h] += 1.
+The caches and lengths are updated in place; the new K/V may be any of bf16 / f16 / fp32 and are
+rounded to the cache dtype (round to nearest even, as ``Tensor.to``).
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _native as N
+
+_FLOAT_DTYPES = {torch.bfloat16: N.DTYPE_BF16, torch.float16: N.DTYPE_F16, torch.float32: N.DTYPE_F32}
+_LEN_DTYPES = {torch.int32: N.DTYPE_I32, torch.int64: N.DTYPE_I64}
+_FLAG_DTYPES = {torch.bool: N.DTYPE_U8, torch.uint8: N.DTYPE_U8, torch.int8: N.DTYPE_U8,
+                torch.int32: N.DTYPE_I32, torch.int64: N.DTYPE_I64}
+
+
+def _cache_strides(t: Tensor):
+    assert t.dim() == 4 and t.stride(3) == 1, "KV caches must be [B, H, storage, D] with a contiguous D axis"
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def _new_strides(t: Tensor):
+    assert t.dim() == 3 and t.stride(2) == 1, "new K/V must be [B, H, D] with a contiguous D axis"
+    return t.stride(0), t.stride(1)
+
+
+def fused_sps_kv_update(
+    *,
+    nw_k: Tensor,
+    nw_v: Tensor,
+    nw_len: Tensor,
+    nw_pos: Tensor,
+    br_k: Tensor,
+    br_v: Tensor,
+    br_len: Tensor,
+    k_window_BxHxD: Tensor,
+    v_window_BxHxD: Tensor,
+    k_retained_BxHxD: Tensor,
+    v_retained_BxHxD: Tensor,
+    active_mask_B: Tensor,
+    window_tokens: int,
+) -> None:
+    """One-launch KV update of one decode layer (see the module docstring)."""
+    batch_size, n_head, head_dim = k_retained_BxHxD.shape
+    window_tokens = int(window_tokens)
+    use_ring = window_tokens > 0
+    assert br_k.shape == br_v.shape, "br.k/v shape mismatch"
+    assert br_k.size(0) == batch_size and br_k.size(1) == n_head and br_k.size(3) == head_dim
+    assert br_len.shape == (batch_size, n_head)
+    assert v_retained_BxHxD.shape == k_retained_BxHxD.shape
+    if use_ring:
+        assert nw_k.shape == nw_v.shape, "nw.k/v shape mismatch"
+        assert nw_k.size(0) == batch_size and nw_k.size(1) == n_head and nw_k.size(3) == head_dim
+        assert nw_len.shape == (batch_size,)
+        assert nw_pos.shape == (batch_size,)
+        assert k_window_BxHxD.shape == k_retained_BxHxD.shape and v_window_BxHxD.shape == k_retained_BxHxD.shape
+        assert nw_k.dtype == br_k.dtype, "ring and retained caches must share a dtype"
+        assert nw_len.dtype == br_len.dtype and nw_pos.dtype == br_len.dtype, "lengths must share a dtype"
+        assert window_tokens <= nw_k.size(2), "window_tokens exceeds the ring storage"
+    tensors = [br_k, br_v, br_len, k_retained_BxHxD, v_retained_BxHxD, active_mask_B]
+    if use_ring:
+        tensors += [nw_k, nw_v, nw_len, nw_pos, k_window_BxHxD, v_window_BxHxD]
+    assert all(t.is_cuda for t in tensors), "fused_sps_kv_update: every tensor must be on the GPU"
+    assert br_k.dtype in _FLOAT_DTYPES, f"unsupported cache dtype {br_k.dtype}"
+    assert br_len.dtype in _LEN_DTYPES, f"lengths must be int32 or int64, got {br_len.dtype}"
+    assert active_mask_B.dim() == 1 and active_mask_B.numel() == batch_size
+    assert active_mask_B.dtype in _FLAG_DTYPES, f"unsupported active-mask dtype {active_mask_B.dtype}"
+
+    new_dtype = k_retained_BxHxD.dtype
+    assert new_dtype in _FLOAT_DTYPES, f"unsupported K/V dtype {new_dtype}"
+    new = [k_retained_BxHxD, v_retained_BxHxD] + ([k_window_BxHxD, v_window_BxHxD] if use_ring else [])
+    new = [t if t.dtype == new_dtype else t.to(new_dtype) for t in new]
+    kr, vr = new[0], new[1]
+    kw, vw = (new[2], new[3]) if use_ring else (kr, vr)
+    ns = _new_strides(kw) + _new_strides(vw) + _new_strides(kr) + _new_strides(vr)
+    ret_st = _cache_strides(br_k) + _cache_strides(br_v)
+    if use_ring:
+        ring_st = _cache_strides(nw_k) + _cache_strides(nw_v)
+        ring = (nw_k.data_ptr(), nw_v.data_ptr(), N.i64_array(ring_st), nw_k.size(2), window_tokens,
+                nw_len.data_ptr(), nw_pos.data_ptr(), N.i64_array((nw_len.stride(0), nw_pos.stride(0))))
+    else:
+        ring = (None, None, N.i64_array((0,) * 6), 0, 0, None, None, N.i64_array((0, 0)))
+    status = N.lib().sps_kv_update(
+        batch_size, n_head, head_dim, _FLOAT_DTYPES[br_k.dtype],
+        *ring,
+        br_k.data_ptr(), br_v.data_ptr(), N.i64_array(ret_st), br_k.size(2),
+        br_len.data_ptr(), N.i64_array((br_len.stride(0), br_len.stride(1))), _LEN_DTYPES[br_len.dtype],
+        _FLOAT_DTYPES[new_dtype], kw.data_ptr(), vw.data_ptr(), kr.data_ptr(), vr.data_ptr(), N.i64_array(ns),
+        active_mask_B.data_ptr(), _FLAG_DTYPES[active_mask_B.dtype], active_mask_B.stride(0),
+        torch.cuda.current_stream(br_k.device).cuda_stream,
+    )
+    N.check("sps_kv_update", status)

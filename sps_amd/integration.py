@@ -12,10 +12,13 @@ module paths and names:
     modeling.models.utils.decode_attention.{KVSegment, masked_kv_attention,
         triton_segmented_q1_attention, triton_segmented_q2_attention}
         (reverse_sps/inference.py:19-23, full_attention_model.py:41)
+    modeling.models.utils.decode_attention_fast.fused_sps_kv_update
+        (reverse_sps/inference.py:24)
 
-``install_into_modeling()`` registers modules under the three attention paths whose functions are
-sps_amd's, and rebinds the names in any of the consumer modules already imported. Call it before
-(or after) importing the modeling package; it never imports Triton or the reference kernels.
+``install_into_modeling()`` registers modules under the three attention paths and the KV-update
+path whose functions are sps_amd's, and rebinds the names in any of the consumer modules already
+imported. Call it before (or after) importing the modeling package; it never imports Triton or the
+reference kernels.
 """
 
 from __future__ import annotations
@@ -25,6 +28,7 @@ import types
 
 from . import attention as _attn
 from . import decode_attention as _dec
+from . import decode_attention_fast as _fast
 
 _ATTENTION_MODULES = {
     "modeling.models.attention.triton_sps_flash_attention": {"sps_sliding_attention": _attn.sps_sliding_attention},
@@ -32,6 +36,7 @@ _ATTENTION_MODULES = {
         "reverse_sps_sliding_attention": _attn.reverse_sps_sliding_attention
     },
     "modeling.models.attention.triton_full_flash_attention": {"full_attention": _attn.full_attention},
+    "modeling.models.utils.decode_attention_fast": {"fused_sps_kv_update": _fast.fused_sps_kv_update},
 }
 
 _DECODE_NAMES = {
@@ -54,6 +59,7 @@ _CONSUMERS = {
         "KVSegment": _dec.KVSegment,
         "masked_kv_attention": _dec.masked_kv_attention,
         "triton_segmented_q2_attention": _dec.triton_segmented_q2_attention,
+        "fused_sps_kv_update": _fast.fused_sps_kv_update,
     },
 }
 

@@ -111,3 +111,21 @@ def test_backward_pass_selector_validation():
                                    p, st, p, st, p, st, None, N.DTYPE_I64, 0, 0.125, 4, 0, -1, None, 0, None)
         assert rc == N.SPS_E_INVALID, bad
         assert "pass selector" in N.last_error()
+
+
+def _kv_update(window=2, ring_storage=4, kv_dtype=N.DTYPE_BF16, new_dtype=N.DTYPE_BF16, len_dtype=N.DTYPE_I64,
+               active_dtype=N.DTYPE_U8, ret_k=0x3000, B=1):
+    z = N.i64_array([0] * 8)
+    p = 0x1000
+    return N.lib().sps_kv_update(B, 1, 64, kv_dtype, p, p, z, ring_storage, window, p, p, z, ret_k, p, z, 8, p, z,
+                                 len_dtype, new_dtype, p, p, p, p, z, p, active_dtype, 1, None)
+
+
+def test_kv_update_argument_validation():
+    assert _kv_update(window=5, ring_storage=4) == N.SPS_E_INVALID and "ring storage" in N.last_error()
+    assert _kv_update(kv_dtype=N.DTYPE_I32) == N.SPS_E_UNSUPPORTED and "cache dtype" in N.last_error()
+    assert _kv_update(new_dtype=N.DTYPE_I64) == N.SPS_E_UNSUPPORTED and "new K/V" in N.last_error()
+    assert _kv_update(len_dtype=N.DTYPE_F32) == N.SPS_E_INVALID and "lengths" in N.last_error()
+    assert _kv_update(active_dtype=N.DTYPE_BF16) == N.SPS_E_INVALID and "active mask" in N.last_error()
+    assert _kv_update(ret_k=None) == N.SPS_E_INVALID and "null pointer" in N.last_error()
+    assert _kv_update(B=0) == N.SPS_OK
