@@ -80,6 +80,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   float lse = qvalid ? a.lse[rowid] : 0.f;
   lse = lse == -INFINITY ? 0.f : lse;  // a query with no visible key: every score is masked to -inf
 
+  // Q pre-scaled by sm_scale * log2(e) (rounded to the input type) and the offsets folded into the
+  // MFMA accumulators: the S tile comes out as S * scale2 - lse and the dP tile as dP - Delta, so
+  // P = exp2(S') and dS = P * dP' cost one VALU operation per element each.
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) qf[c] = scale_frag<E>(qf[c], a.scale2);
+  const f32x16_t c_s = f32x16_t{} - lse, c_dp = f32x16_t{} - delta;
+
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
 #pragma unroll
@@ -139,7 +146,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
         if ((act2 >> y) & 1) {
           const uint16_t* tK = sK[buf][y];
           const uint16_t* tV = sV[buf][y];
-          f32x16_t sc = {}, dp = {};
+          f32x16_t sc = c_s, dp = c_dp;
 #pragma unroll
           for (int c = 0; c < D / 16; ++c) {
             sc = E::mfma(lds_read_b128(tK + c32 * G::RS + 16 * c + 8 * g), qf[c], sc);
@@ -151,9 +158,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
           uint32_t dsk[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float p0 = fast_exp2(fmaf(sc[2 * e], a.scale2, -lse));
-            const float p1 = fast_exp2(fmaf(sc[2 * e + 1], a.scale2, -lse));
-            dsk[e] = E::pack2(p0 * (dp[2 * e] - delta), p1 * (dp[2 * e + 1] - delta));
+            const float p0 = fast_exp2(sc[2 * e]);
+            const float p1 = fast_exp2(sc[2 * e + 1]);
+            dsk[e] = E::pack2(p0 * dp[2 * e], p1 * dp[2 * e + 1]);
           }
 #pragma unroll
           for (int dc = 0; dc < G::DC; ++dc) {
@@ -239,6 +246,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
       vf[c] = kvalid ? *reinterpret_cast<const u32x4_t*>(vrow + 16 * c + 8 * g) : z;
     }
   }
+  // K pre-scaled by sm_scale * log2(e) (rounded to the input type); the S and dP tiles start from
+  // -LSE and -Delta of their query rows, so they come out of the MFMAs as S * scale2 - LSE and
+  // dP - Delta: P = exp2(S') and dS = P * dP' cost one VALU operation per element each.
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) kf[c] = scale_frag<E>(kf[c], a.scale2);
 
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
@@ -306,7 +318,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
         if ((act2 >> y) & 1) {
           const uint16_t* tQ = sQ[buf][y];
           const uint16_t* tDO = sDO[buf][y];
-          f32x16_t sc = {}, dp = {};
+          f32x16_t sc, dp;
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) {
+            // Query rows 8*i4 + 4g + {0..3} of this chunk.
+            const f32x4_t l4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
+                (const SPS_LDS float*)(&sLse[buf][y][8 * i4 + 4 * g]));
+            const f32x4_t d4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
+                (const SPS_LDS float*)(&sDelta[buf][y][8 * i4 + 4 * g]));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              sc[4 * i4 + t] = -l4[t];
+              dp[4 * i4 + t] = -d4[t];
+            }
+          }
 #pragma unroll
           for (int c = 0; c < D / 16; ++c) {
             sc = E::mfma(lds_read_b128(tQ + c32 * G::RS + 16 * c + 8 * g), kf[c], sc);
@@ -318,17 +343,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
           uint32_t pk[8], dsk[8];
 #pragma unroll
           for (int i4 = 0; i4 < 4; ++i4) {
-            // Query rows 8*i4 + 4g + {0..3} of this chunk.
-            const f32x4_t l4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                (const SPS_LDS float*)(&sLse[buf][y][8 * i4 + 4 * g]));
-            const f32x4_t d4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                (const SPS_LDS float*)(&sDelta[buf][y][8 * i4 + 4 * g]));
             float p[4], ds[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
               const int e = 4 * i4 + t;
-              p[t] = fast_exp2(fmaf(sc[e], a.scale2, -l4[t]));
-              ds[t] = p[t] * (dp[e] - d4[t]);
+              p[t] = fast_exp2(sc[e]);
+              ds[t] = p[t] * dp[e];
             }
             pk[2 * i4] = E::pack2(p[0], p[1]);
             pk[2 * i4 + 1] = E::pack2(p[2], p[3]);
