@@ -15,13 +15,13 @@ struct DecodeGeom {
   static constexpr int EPL = 16 / BYTES;
   static constexpr int LPR = D / EPL;
   static constexpr int RPP = 64 / LPR;
-  static constexpr int PASS = 8;
+  static constexpr int PASS = 16;
   static constexpr int CHUNK = 4 * RPP * PASS;
   static constexpr int REC = D + 4;  // floats per partial record: acc[D], m, l, 2 pad
 };
 
 // Host-side helper with the same numbers (the kernels static_assert agreement).
-inline int decode_chunk_keys(int D, int kv_bytes) { return 4 * (64 / (D / (16 / kv_bytes))) * 8; }
+inline int decode_chunk_keys(int D, int kv_bytes) { return 4 * (64 / (D / (16 / kv_bytes))) * 16; }
 inline int decode_record_floats(int D) { return D + 4; }
 
 struct DecodeSeg {

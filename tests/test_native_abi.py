@@ -78,7 +78,8 @@ def test_workspace_sizes():
     assert bwd >= with_docs + 4 * 16 * 4096 * 4
     scans = N.i64_array([64, 4096])
     dec = lib.sps_decode_workspace_bytes(64, 16, 64, 1, N.DTYPE_BF16, 2, scans)
-    assert dec >= 64 * 16 * (1 + 16) * (64 + 4) * 4
+    # D = 64 bf16: 512-key chunks (4 waves x 8 rows x 16 passes) -> 1 + 8 chunks of (64 + 4) floats.
+    assert dec >= 64 * 16 * (1 + 8) * (64 + 4) * 4
 
 
 def _decode(nq=1, D=64, n_seg=0, q_dtype=N.DTYPE_BF16, extra_dtype=N.DTYPE_BF16, n_extra=0):
