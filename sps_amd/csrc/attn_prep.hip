@@ -51,22 +51,29 @@ __device__ int k_tile_cost(const MaskSpec& m, const RunBounds& rb, int kt) {
   return blocks_in(k0, key_last_query(m, stream, k1, rb.end(k1)));
 }
 
-// Exclusive scans over the per-thread chunk summaries (Hillis-Steele in LDS).
+// Exclusive scan of the per-thread chunk summaries in thread order (reverse: in reverse thread
+// order) for an associative, commutative op: a shuffle scan inside each wave, then the waves'
+// totals through LDS (two barriers in all).
+constexpr int kPrepWaves = kPrepThreads / 64;
+
 template <class Op>
 __device__ int block_exclusive_scan(int* s, int x, int identity, Op op, bool reverse) {
-  const int tid = threadIdx.x;
-  const int slot = reverse ? kPrepThreads - 1 - tid : tid;
-  s[slot] = x;
-  __syncthreads();
-  for (int o = 1; o < kPrepThreads; o <<= 1) {
-    const int y = slot >= o ? s[slot - o] : identity;
-    __syncthreads();
-    s[slot] = op(s[slot], y);
-    __syncthreads();
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int v = x;  // inclusive scan within the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = reverse ? __shfl_down(v, o) : __shfl_up(v, o);
+    if (reverse ? lane + o < 64 : lane >= o) v = op(v, y);
   }
-  const int r = slot > 0 ? s[slot - 1] : identity;
+  const int wslot = reverse ? kPrepWaves - 1 - wave : wave;
+  if (reverse ? lane == 0 : lane == 63) s[wslot] = v;
   __syncthreads();
-  return r;
+  int carry = identity;
+  for (int w = 0; w < wslot; ++w) carry = op(carry, s[w]);
+  int ex = reverse ? __shfl_down(v, 1) : __shfl_up(v, 1);
+  if (reverse ? lane == 63 : lane == 0) ex = identity;
+  __syncthreads();  // the wave totals may be overwritten by the next scan
+  return op(carry, ex);
 }
 
 // Writes the order of `n` tiles by decreasing cost (ties: lower index first) into order[0..n).
@@ -86,7 +93,7 @@ __device__ void sort_tiles(const int* cost, int n, int* order, bool ascending_fa
 
 __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs a) {
   __shared__ int s_scan[kPrepThreads];
-  __shared__ int s_cost[kMaxSortTiles];
+  __shared__ int s_cost[kMaxSortTiles], s_cost_k[kMaxSortTiles];
   __shared__ int s_nonmono;
   __shared__ short s_start[kLdsRow], s_end[kLdsRow];
   const MaskSpec m = a.m;
@@ -185,17 +192,16 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   const bool lds_ok = in_regs;
   const RunBounds rb = {lds_ok ? s_start : nullptr, lds_ok ? s_end : nullptr, start, end};
 
+  // Query-tile and key-tile orders (independent: both cost passes, one barrier, both sorts).
   const int nqt = q_tiles(N);
+  const int nkt = k_tiles(m.family, N, m.P);
   if (nqt <= kMaxSortTiles)
     for (int t = tid; t < nqt; t += kPrepThreads) s_cost[t] = q_tile_cost(m, rb, t);
+  if (nkt <= kMaxSortTiles)
+    for (int t = tid; t < nkt; t += kPrepThreads) s_cost_k[t] = k_tile_cost(m, rb, t);
   __syncthreads();
   sort_tiles(s_cost, nqt, a.q_order + (int64_t)b * nqt, false);
-  __syncthreads();
-  const int nkt = k_tiles(m.family, N, m.P);
-  if (nkt <= kMaxSortTiles)
-    for (int t = tid; t < nkt; t += kPrepThreads) s_cost[t] = k_tile_cost(m, rb, t);
-  __syncthreads();
-  sort_tiles(s_cost, nkt, a.k_order + (int64_t)b * nkt, true);
+  sort_tiles(s_cost_k, nkt, a.k_order + (int64_t)b * nkt, true);
 }
 
 hipError_t launch_row_layout(const AttnArgs& a, hipStream_t stream) {
