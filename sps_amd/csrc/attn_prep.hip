@@ -76,17 +76,27 @@ __device__ int block_exclusive_scan(int* s, int x, int identity, Op op, bool rev
   return op(carry, ex);
 }
 
-// Writes the order of `n` tiles by decreasing cost (ties: lower index first) into order[0..n).
-__device__ void sort_tiles(const int* cost, int n, int* order, bool ascending_fallback) {
-  const int tid = threadIdx.x;
+// Writes the order of `n` tiles by decreasing cost (ties: lower index first) into order[0..n),
+// with threads [first, first + count) of the workgroup (rank sort; the cost reads are batched so
+// their LDS latencies overlap).
+__device__ void sort_tiles(const int* cost, int n, int* order, bool ascending_fallback, int first, int count) {
+  const int tid = threadIdx.x - first;
+  if (tid < 0 || tid >= count) return;
   if (n > kMaxSortTiles) {
-    for (int t = tid; t < n; t += kPrepThreads) order[t] = ascending_fallback ? t : n - 1 - t;
+    for (int t = tid; t < n; t += count) order[t] = ascending_fallback ? t : n - 1 - t;
     return;
   }
-  for (int t = tid; t < n; t += kPrepThreads) {
+  for (int t = tid; t < n; t += count) {
     const int c = cost[t];
-    int r = 0;
-    for (int j = 0; j < n; ++j) r += (cost[j] > c) || (cost[j] == c && j < t);
+    int r = 0, j = 0;
+    for (; j + 8 <= n; j += 8) {
+      int x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = cost[j + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) r += (x[u] > c) || (x[u] == c && j + u < t);
+    }
+    for (; j < n; ++j) r += (cost[j] > c) || (cost[j] == c && j < t);
     order[r] = t;
   }
 }
@@ -200,8 +210,8 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   if (nkt <= kMaxSortTiles)
     for (int t = tid; t < nkt; t += kPrepThreads) s_cost_k[t] = k_tile_cost(m, rb, t);
   __syncthreads();
-  sort_tiles(s_cost, nqt, a.q_order + (int64_t)b * nqt, false);
-  sort_tiles(s_cost_k, nkt, a.k_order + (int64_t)b * nkt, true);
+  sort_tiles(s_cost, nqt, a.q_order + (int64_t)b * nqt, false, 0, kPrepThreads / 2);
+  sort_tiles(s_cost_k, nkt, a.k_order + (int64_t)b * nkt, true, kPrepThreads / 2, kPrepThreads / 2);
 }
 
 hipError_t launch_row_layout(const AttnArgs& a, hipStream_t stream) {
