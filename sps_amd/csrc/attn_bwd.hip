@@ -24,11 +24,17 @@ namespace sps {
 // Pairs of blocks whose loads are in flight while a pair is computed (run_pairs).
 constexpr int kLook = 1;
 
+// Blocks per barrier (LDS budget: both passes run 2 workgroups per CU, so four 32-row blocks of
+// two tensors, double-buffered, fit; fewer barriers per block than pairs).
+constexpr int kDqGroup = 4;
+constexpr int kDkdvGroup = 4;
+
 template <int D, class E>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][2][G::ELEMS];  // [buffer][block of the pair]
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][2][G::ELEMS];
+  constexpr int NG = kDqGroup;
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][NG][G::ELEMS];  // [buffer][block of the group]
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][NG][G::ELEMS];
   __shared__ int s_span[4 * kWaves];
 
   const MaskSpec m = a.m;
@@ -90,7 +96,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
+    for (int y = 0; y < NG; ++y) {
       zero_pad_cols<D>(sK[x][y], tid);
       zero_pad_cols<D>(sV[x][y], tid);
     }
@@ -103,11 +109,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   const uint32_t k_c0 = (uint32_t)(c0 * a.sk.n * 2), k_c1 = (uint32_t)(c1 * a.sk.n * 2);
   const uint32_t v_c0 = (uint32_t)(c0 * a.sv.n * 2), v_c1 = (uint32_t)(c1 * a.sv.n * 2);
 
-  TileRegs<D> rk[kLook][2], rv[kLook][2];
+  TileRegs<D> rk[kLook][NG], rv[kLook][NG];
   auto issue = [&](int j, int slot) {
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      const int i = 2 * j + y;
+    for (int y = 0; y < NG; ++y) {
+      const int i = NG * j + y;
       if (i < nb) {
         const bool s0 = i < plan.n0;
         rk[slot][y].load(k_src, (uint32_t)i * k_blk + (s0 ? k_c0 : k_c1), k_off, tid);
@@ -117,7 +123,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   };
   auto put = [&](int slot, int buf) {
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
+    for (int y = 0; y < NG; ++y) {
       rk[slot][y].store(sK[buf][y], tid);
       rv[slot][y].store(sV[buf][y], tid);
     }
@@ -133,12 +139,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
       return classify_block(i < plan.n0 ? st.w0 : st.w1, plan.first(i), EXACT);
     };
     const BlockMask bm = build_block_mask(nb, cls_of);
-    run_pairs<kLook>(nb, issue, put, [&](int j, int buf) {
+    run_groups<kLook, NG>(nb, issue, put, [&](int j, int buf) {
       int act2, full2;
-      pair_codes(bm, 2 * j, nb, cls_of, act2, full2);
+      group_codes<NG>(bm, NG * j, nb, cls_of, act2, full2);
 #pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        const int i = 2 * j + y;
+      for (int y = 0; y < NG; ++y) {
+        const int i = NG * j + y;
         const bool s0 = i < plan.n0;
         const int t0 = plan.first(i);
         const WaveSpan ws = s0 ? st.w0 : st.w1;
@@ -207,10 +213,11 @@ struct ChunkRegs {
 template <int D, class E>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][2][G::ELEMS];  // [buffer][chunk of the pair]
-  __shared__ __attribute__((aligned(16))) uint16_t sDO[2][2][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) float sLse[2][2][kBlock];
-  __shared__ __attribute__((aligned(16))) float sDelta[2][2][kBlock];
+  constexpr int NG = kDkdvGroup;
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][NG][G::ELEMS];  // [buffer][chunk of the group]
+  __shared__ __attribute__((aligned(16))) uint16_t sDO[2][NG][G::ELEMS];
+  __shared__ __attribute__((aligned(16))) float sLse[2][NG][kBlock];
+  __shared__ __attribute__((aligned(16))) float sDelta[2][NG][kBlock];
   __shared__ int s_span[2 * kWaves];
 
   const MaskSpec m = a.m;
@@ -255,7 +262,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
+    for (int y = 0; y < NG; ++y) {
       zero_pad_cols<D>(sQ[x][y], tid);
       zero_pad_cols<D>(sDO[x][y], tid);
     }
@@ -266,11 +273,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   const uint32_t q_c0 = (uint32_t)((int64_t)st.c0 * kBlock * a.sq.n * 2);
   const uint32_t o_c0 = (uint32_t)((int64_t)st.c0 * kBlock * a.sdo.n * 2);
 
-  ChunkRegs<D> rc[kLook][2];
+  ChunkRegs<D> rc[kLook][NG];
   auto issue = [&](int j, int slot) {
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
-      const int i = 2 * j + y;
+    for (int y = 0; y < NG; ++y) {
+      const int i = NG * j + y;
       if (i < nc) {
         rc[slot][y].q.load(q_src, q_c0 + (uint32_t)i * q_blk, q_off, tid);
         rc[slot][y].o.load(o_src, o_c0 + (uint32_t)i * o_blk, o_off, tid);
@@ -286,7 +293,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   };
   auto put = [&](int slot, int buf) {
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
+    for (int y = 0; y < NG; ++y) {
       rc[slot][y].q.store(sQ[buf][y], tid);
       rc[slot][y].o.store(sDO[buf][y], tid);
       if (tid < kBlock) {
@@ -308,12 +315,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
     constexpr bool EXACT = decltype(exact_tag)::value;
     auto cls_of = [&](int i) { return classify_block(st.w, (st.c0 + i) * kBlock, EXACT); };
     const BlockMask bm = build_block_mask(nc, cls_of);
-    run_pairs<kLook>(nc, issue, put, [&](int j, int buf) {
+    run_groups<kLook, NG>(nc, issue, put, [&](int j, int buf) {
       int act2, full2;
-      pair_codes(bm, 2 * j, nc, cls_of, act2, full2);
+      group_codes<NG>(bm, NG * j, nc, cls_of, act2, full2);
 #pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        const int i = 2 * j + y;
+      for (int y = 0; y < NG; ++y) {
+        const int i = NG * j + y;
         const int qc = (st.c0 + i) * kBlock;
         if ((act2 >> y) & 1) {
           const uint16_t* tQ = sQ[buf][y];

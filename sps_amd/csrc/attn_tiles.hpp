@@ -307,34 +307,42 @@ __device__ __forceinline__ BlockMask build_block_mask(int nb, ClassFn cls_of) {
   return bm;
 }
 
-// Two-bit activity and fullness codes of blocks i, i + 1 (i even; blocks >= nb are SKIP).
-template <class ClassFn>
-__device__ __forceinline__ void pair_codes(const BlockMask& bm, int i, int nb, ClassFn cls_of, int& act2, int& full2) {
+// G-bit activity and fullness codes of blocks i .. i + G - 1 (i a multiple of G, G a power of two
+// <= 8; blocks >= nb are SKIP).
+template <int G, class ClassFn>
+__device__ __forceinline__ void group_codes(const BlockMask& bm, int i, int nb, ClassFn cls_of, int& act, int& full) {
+  constexpr uint64_t kMask = (1ull << G) - 1;
   if (i < 128) {
     const int sh = i & 63;
-    act2 = (int)(((i < 64 ? bm.act0 : bm.act1) >> sh) & 3ull);
-    full2 = (int)(((i < 64 ? bm.full0 : bm.full1) >> sh) & 3ull);
+    act = (int)(((i < 64 ? bm.act0 : bm.act1) >> sh) & kMask);
+    full = (int)(((i < 64 ? bm.full0 : bm.full1) >> sh) & kMask);
   } else {
-    act2 = full2 = 0;
+    act = full = 0;
 #pragma unroll
-    for (int y = 0; y < 2; ++y) {
+    for (int y = 0; y < G; ++y) {
       const int c = i + y < nb ? cls_of(i + y) : TILE_SKIP;
-      act2 |= (c != TILE_SKIP) << y;
-      full2 |= (c == TILE_FULL) << y;
+      act |= (c != TILE_SKIP) << y;
+      full |= (c == TILE_FULL) << y;
     }
   }
 }
 
-// Software pipeline over `nb` blocks taken in pairs (64 stream rows per iteration, one barrier per
-// pair). issue(j, slot) starts the global loads of pair j into register slot `slot` (of L),
-// put(slot, buf) writes a slot to LDS buffer `buf` (0/1), body(j, buf) computes pair j from LDS
-// buffer `buf`. Pair j + 1 + L is loaded while pair j is computed and reaches LDS L iterations
-// later, so each pair's loads have L full iterations to land. Unrolled by two, so slots and
-// buffers are compile-time indices.
-template <int L, class Issue, class Put, class Body>
-__device__ __forceinline__ void run_pairs(int nb, Issue&& issue, Put&& put, Body&& body) {
-  static_assert(L == 1 || L == 2, "lookahead of one or two pairs");
-  const int np = (nb + 1) >> 1;
+// Two-bit codes of blocks i, i + 1 (i even).
+template <class ClassFn>
+__device__ __forceinline__ void pair_codes(const BlockMask& bm, int i, int nb, ClassFn cls_of, int& act2, int& full2) {
+  group_codes<2>(bm, i, nb, cls_of, act2, full2);
+}
+
+// Software pipeline over `nb` blocks taken in groups of G (32·G stream rows per iteration, one
+// barrier per group). issue(j, slot) starts the global loads of group j into register slot `slot`
+// (of L), put(slot, buf) writes a slot to LDS buffer `buf` (0/1), body(j, buf) computes group j
+// from LDS buffer `buf`. Group j + 1 + L is loaded while group j is computed and reaches LDS L
+// iterations later, so each group's loads have L full iterations to land. Unrolled by two, so
+// slots and buffers are compile-time indices. run_pairs is the G = 2 form.
+template <int L, int G = 2, class Issue, class Put, class Body>
+__device__ __forceinline__ void run_groups(int nb, Issue&& issue, Put&& put, Body&& body) {
+  static_assert(L == 1 || L == 2, "lookahead of one or two groups");
+  const int np = (nb + G - 1) / G;
   if (np > 0) {
     issue(0, 0);
     put(0, 0);
@@ -356,6 +364,11 @@ __device__ __forceinline__ void run_pairs(int nb, Issue&& issue, Put&& put, Body
       }
     }
   }
+}
+
+template <int L, class Issue, class Put, class Body>
+__device__ __forceinline__ void run_pairs(int nb, Issue&& issue, Put&& put, Body&& body) {
+  run_groups<L, 2>(nb, issue, put, body);
 }
 
 // Maximum of the 32 elements of two accumulators as a shallow tree of 3-input maxima (the loops
