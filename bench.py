@@ -169,6 +169,53 @@ def bench_attention(cfg, steps: int, warmup: int):
     }
 
 
+def bench_pre_attention(cfg, steps: int):
+    """The attention modules' pre-attention step at the C3 shape (sps/core.py:45-55): RoPE on Q and K
+    of a packed fp32 QKV projection and the bf16 casts, fused in one launch, next to the reference's
+    op sequence (apply_rotary_emb in torch, transposes, casts) on the same GPU."""
+    import torch
+
+    from sps_amd import rope as SR
+
+    B, T2, H, D = cfg.batch, cfg.n, cfg.heads, cfg.head_dim
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn(B, T2, 3 * H * D, generator=g).cuda()
+    q, k, v = (t.view(B, T2, H, D) for t in qkv.split(H * D, dim=2))
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2)[: D // 2].float() / D))
+    freqs = torch.polar(torch.ones(T2, D // 2), torch.outer(torch.arange(T2).float(), inv)).cuda()
+
+    def fused():
+        SR.rope_qkv_for_attention(q, k, v, freqs)
+
+    def reference_ops():
+        zq = torch.view_as_complex(q.float().reshape(B, T2, H, -1, 2))
+        zk = torch.view_as_complex(k.float().reshape(B, T2, H, -1, 2))
+        f = freqs.view(1, T2, 1, D // 2)
+        qr = torch.view_as_real(zq * f).flatten(3).type_as(q)
+        kr = torch.view_as_real(zk * f).flatten(3).type_as(k)
+        return qr.transpose(1, 2).to(torch.bfloat16), kr.transpose(1, 2).to(torch.bfloat16), \
+            v.transpose(1, 2).to(torch.bfloat16)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    us = timed(fused)
+    ref_us = timed(reference_ops)
+    nbytes = 3 * B * T2 * H * D * (4 + 2) + T2 * D * 4  # read fp32 q, k, v (+ freqs), write bf16
+    return {"workload": "C3 pre-attention: RoPE(q, k) + bf16 casts of a [4, 4096, 3*1024] fp32 projection",
+            "us": round(us, 2), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "reference_ops_us": round(ref_us, 2), "algorithmic_bytes": nbytes}
+
+
 def cpu_attention_baseline(cfg, budget_s: float):
     """Reference CPU path (dense masked SDPA fwd + autograd bwd, fp32) on whole batch rows of the same
     inputs until `budget_s` seconds are spent (at least one row)."""
@@ -377,6 +424,8 @@ def main() -> int:
     log(f"C3 fwd+bwd: {args.warmup} warm-up + {args.steps} timed steps")
     att = bench_attention(C3, args.steps, args.warmup)
     log(f"C3: {att['value']:.1f} TFLOP/s, {att['ms_per_step']:.3f} ms/step, kernels {att['kernels']}")
+    pre = bench_pre_attention(C3, 20)
+    log(f"C3 pre-attention (fused RoPE + casts): {pre}")
     dec = None
     if not args.no_decode:
         log(f"C5 decode: {args.decode_steps} timed steps")
@@ -414,6 +463,7 @@ def main() -> int:
         "kernels": att["kernels"],
         "roofline": att["roofline"],
         "cpu_baseline": cpu,
+        "pre_attention": pre,
         "decode": dec,
     }
     print(json.dumps(line), flush=True)

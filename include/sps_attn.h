@@ -24,6 +24,8 @@
  *   sps_decode                    <- triton_segmented_q1_attention (utils/decode_attention.py:393-480),
  *                                    triton_segmented_q2_attention (utils/decode_attention.py:483-594)
  *   sps_kv_update                 <- fused_sps_kv_update (utils/decode_attention_fast.py:139-221)
+ *   sps_rope_qkv                  <- apply_rotary_emb (model.py:201-230) + the transposes and casts
+ *                                    before the attention call (sps/core.py:45-55)
  *   sps_attn_mask                 <- the mask block of _attn_fwd_inner_sps
  *                                    (attention/triton_sps_flash_attention.py:70-111); a
  *                                    verification entry point that materialises the mask the
@@ -205,6 +207,24 @@ int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v,
                   const void* k_window, const void* v_window, const void* k_retained, const void* v_retained,
                   const int64_t* new_strides, const void* active, int active_dtype, int64_t active_stride,
                   void* stream);
+
+/*
+ * Pre-attention rotary embedding and cast, one pass (replaces apply_rotary_emb, model.py:201-230,
+ * and the transposes / .to(bfloat16) of the attention callers, sps/core.py:45-55,
+ * reverse_sps/core.py:60-75). For every (b, n, h) row and pair i < D/2:
+ *   out[2i]   = x[2i] * f.re - x[2i+1] * f.im,   out[2i+1] = x[2i] * f.im + x[2i+1] * f.re
+ * in fp32 with f = freqs[b, n, i] (complex, stored as (re, im) float pairs; freqs_strides =
+ * {b, n} in floats, b = 0 when all sequences share the positions), applied to Q and K; V (may be
+ * null) is copied. Results are rounded once to out_dtype (round to nearest even). Inputs
+ * [B, N, H, D] of in_dtype with element strides {b, n, h}; outputs likewise (any layout with a
+ * contiguous D axis: [B, N, H, D] memory is what the attention entry points take as [B, H, N, D]
+ * views). Every row start must be 16-byte aligned; D a multiple of 8.
+ */
+int sps_rope_qkv(int B, int N, int H, int D, int in_dtype, const void* q, const int64_t* q_strides, const void* k,
+                 const int64_t* k_strides, const void* v, const int64_t* v_strides, const float* freqs,
+                 const int64_t* freqs_strides, int out_dtype, void* q_out, const int64_t* q_out_strides,
+                 void* k_out, const int64_t* k_out_strides, void* v_out, const int64_t* v_out_strides,
+                 void* stream);
 
 #ifdef __cplusplus
 }

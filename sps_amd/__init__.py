@@ -4,6 +4,7 @@ Drop-in replacements for the reference's attention entry points:
   prefill / training: ``sps_sliding_attention``, ``reverse_sps_sliding_attention``, ``full_attention``
   decode:             ``KVSegment``, ``triton_segmented_q1_attention``, ``triton_segmented_q2_attention``,
                       ``masked_kv_attention``, ``fused_sps_kv_update`` (KV-cache update)
+  pre-attention:      ``apply_rotary_emb``, ``rope_qkv_for_attention`` (RoPE + casts + layout, one launch)
   document ids:       ``generate_left_padded_document_idx``
 All compute runs in libsps_attn.so (hand-written HIP kernels); see include/sps_attn.h.
 """
@@ -23,6 +24,7 @@ from .document_idx import (
     validate_left_padded_tokens,
 )
 from .integration import install_into_modeling
+from .rope import apply_rotary_emb, rope_qkv_for_attention
 
 __all__ = [
     "sps_sliding_attention",
@@ -38,4 +40,6 @@ __all__ = [
     "infer_is_real_tokens",
     "validate_left_padded_tokens",
     "install_into_modeling",
+    "apply_rotary_emb",
+    "rope_qkv_for_attention",
 ]

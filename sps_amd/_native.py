@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "sps_decode_workspace_bytes",
     "sps_decode",
     "sps_kv_update",
+    "sps_rope_qkv",
 )
 
 _i32 = C.c_int
@@ -105,6 +106,14 @@ _SIGNATURES = {
         + [_p, _p, _pi64, _i32, _p, _pi64, _i32]  # retained, length dtype
         + [_i32, _p, _p, _p, _p, _pi64]  # new K/V
         + [_p, _i32, _i64, _p],
+    ),
+    "sps_rope_qkv": (
+        _i32,
+        [_i32, _i32, _i32, _i32, _i32]
+        + [_p, _pi64] * 3
+        + [_p, _pi64, _i32]
+        + [_p, _pi64] * 3
+        + [_p],
     ),
 }
 

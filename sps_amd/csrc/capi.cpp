@@ -501,4 +501,62 @@ int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v,
   return hip_status(sps::launch_kv_update(a, static_cast<hipStream_t>(stream)), "kv update");
 }
 
+int sps_rope_qkv(int B, int N, int H, int D, int in_dtype, const void* q, const int64_t* q_strides, const void* k,
+                 const int64_t* k_strides, const void* v, const int64_t* v_strides, const float* freqs,
+                 const int64_t* freqs_strides, int out_dtype, void* q_out, const int64_t* q_out_strides,
+                 void* k_out, const int64_t* k_out_strides, void* v_out, const int64_t* v_out_strides,
+                 void* stream) {
+  g_last_error.clear();
+  if (B < 0 || N < 0 || H < 0 || D < 0) return fail(SPS_E_INVALID, "negative size B=%d N=%d H=%d D=%d", B, N, H, D);
+  auto float_type = [](int t) { return t == SPS_DTYPE_BF16 || t == SPS_DTYPE_F16 || t == SPS_DTYPE_F32; };
+  if (!float_type(in_dtype)) return fail(SPS_E_UNSUPPORTED, "input dtype code %d not supported", in_dtype);
+  if (!float_type(out_dtype)) return fail(SPS_E_UNSUPPORTED, "output dtype code %d not supported", out_dtype);
+  if (D % 8 != 0) return fail(SPS_E_UNSUPPORTED, "head_dim %d must be a multiple of 8", D);
+  if ((int64_t)B * N * H * D == 0) return SPS_OK;
+  if (!q || !k || !freqs || !q_out || !k_out || !q_strides || !k_strides || !freqs_strides || !q_out_strides ||
+      !k_out_strides)
+    return fail(SPS_E_INVALID, "q/k/freqs/outputs: null pointer");
+  if (v && (!v_out || !v_strides || !v_out_strides)) return fail(SPS_E_INVALID, "v output: null pointer");
+  // 16-byte pieces: every row start must be 16-byte aligned in every tensor.
+  const int64_t in_el = in_dtype == SPS_DTYPE_F32 ? 4 : 2, out_el = out_dtype == SPS_DTYPE_F32 ? 4 : 2;
+  auto rows_aligned = [](const void* p, const int64_t* st, int64_t el) {
+    if (!aligned16(p)) return false;
+    for (int i = 0; i < 3; ++i)
+      if ((st[i] * el) % 16 != 0) return false;
+    return true;
+  };
+  if (!rows_aligned(q, q_strides, in_el) || !rows_aligned(k, k_strides, in_el) ||
+      (v && !rows_aligned(v, v_strides, in_el)))
+    return fail(SPS_E_INVALID, "q/k/v rows must start 16-byte aligned (base and strides)");
+  if (!rows_aligned(q_out, q_out_strides, out_el) || !rows_aligned(k_out, k_out_strides, out_el) ||
+      (v && !rows_aligned(v_out, v_out_strides, out_el)))
+    return fail(SPS_E_INVALID, "output rows must start 16-byte aligned (base and strides)");
+  if (!aligned16(freqs) || (freqs_strides[0] * 4) % 16 != 0 || (freqs_strides[1] * 4) % 16 != 0)
+    return fail(SPS_E_INVALID, "freqs rows must start 16-byte aligned");
+  sps::RopeArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.B = B;
+  a.N = N;
+  a.H = H;
+  a.D = D;
+  a.in_dtype = in_dtype;
+  a.out_dtype = out_dtype;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.q_sb = q_strides[0], a.q_sn = q_strides[1], a.q_sh = q_strides[2];
+  a.k_sb = k_strides[0], a.k_sn = k_strides[1], a.k_sh = k_strides[2];
+  if (v) a.v_sb = v_strides[0], a.v_sn = v_strides[1], a.v_sh = v_strides[2];
+  a.freqs = freqs;
+  a.f_sb = freqs_strides[0];
+  a.f_sn = freqs_strides[1];
+  a.qo = q_out;
+  a.ko = k_out;
+  a.vo = v_out;
+  a.qo_sb = q_out_strides[0], a.qo_sn = q_out_strides[1], a.qo_sh = q_out_strides[2];
+  a.ko_sb = k_out_strides[0], a.ko_sn = k_out_strides[1], a.ko_sh = k_out_strides[2];
+  if (v) a.vo_sb = v_out_strides[0], a.vo_sn = v_out_strides[1], a.vo_sh = v_out_strides[2];
+  return hip_status(sps::launch_rope_qkv(a, static_cast<hipStream_t>(stream)), "rope");
+}
+
 }  // extern "C"

@@ -102,4 +102,21 @@ struct KvUpdateArgs {
 
 hipError_t launch_kv_update(const KvUpdateArgs& a, hipStream_t stream);
 
+// Pre-attention rotary embedding of Q and K and cast of Q, K, V (one pass; rope.hip).
+struct RopeArgs {
+  int B, N, H, D;
+  int in_dtype, out_dtype;  // 0 bf16, 1 f16, 2 f32
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t q_sb, q_sn, q_sh, k_sb, k_sn, k_sh, v_sb, v_sn, v_sh;
+  const float* freqs;  // real view of complex64 freqs: [.., N, D/2, 2]
+  int64_t f_sb, f_sn;  // float strides (f_sb = 0: shared by all sequences)
+  void* qo;
+  void* ko;
+  void* vo;
+  int64_t qo_sb, qo_sn, qo_sh, ko_sb, ko_sn, ko_sh, vo_sb, vo_sn, vo_sh;
+};
+hipError_t launch_rope_qkv(const RopeArgs& a, hipStream_t stream);
+
 }  // namespace sps

@@ -64,9 +64,20 @@ _CONSUMERS = {
 }
 
 
-def install_into_modeling() -> list[str]:
-    """Installs the drop-in; returns the module names that were created or patched."""
+def install_into_modeling(rope: bool = False) -> list[str]:
+    """Installs the drop-in; returns the module names that were created or patched.
+
+    ``rope=True`` also rebinds ``modeling.models.model.apply_rotary_emb`` (model.py:201-230, called
+    by every attention module) to sps_amd's GPU kernel. It is opt-in because the reference also
+    runs that function on CPU tensors, which sps_amd does not support."""
     touched = []
+    if rope:
+        from . import rope as _rope
+
+        mod = sys.modules.get("modeling.models.model")
+        if mod is not None:
+            mod.apply_rotary_emb = _rope.apply_rotary_emb
+            touched.append("modeling.models.model")
     for name, attrs in _ATTENTION_MODULES.items():
         mod = sys.modules.get(name)
         if mod is None:

@@ -130,3 +130,17 @@ def test_kv_update_argument_validation():
     assert _kv_update(active_dtype=N.DTYPE_BF16) == N.SPS_E_INVALID and "active mask" in N.last_error()
     assert _kv_update(ret_k=None) == N.SPS_E_INVALID and "null pointer" in N.last_error()
     assert _kv_update(B=0) == N.SPS_OK
+
+
+def _rope(D=64, in_dtype=N.DTYPE_F32, ptr=0x10000, st=(4096, 64, 64)):
+    s = N.i64_array(st)
+    f = N.i64_array((0, 32))
+    return N.lib().sps_rope_qkv(1, 1, 1, D, in_dtype, ptr, s, ptr, s, None, None, 0x20000, f, N.DTYPE_BF16,
+                                0x30000, s, 0x30000, s, None, None, None)
+
+
+def test_rope_argument_validation():
+    assert _rope(D=12) == N.SPS_E_UNSUPPORTED and "multiple of 8" in N.last_error()
+    assert _rope(in_dtype=N.DTYPE_I32) == N.SPS_E_UNSUPPORTED and "input dtype" in N.last_error()
+    assert _rope(ptr=0x10004) == N.SPS_E_INVALID and "aligned" in N.last_error()
+    assert _rope(st=(4096, 66, 64)) == N.SPS_E_INVALID and "aligned" in N.last_error()
