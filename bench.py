@@ -216,6 +216,68 @@ def bench_pre_attention(cfg, steps: int):
             "reference_ops_us": round(ref_us, 2), "algorithmic_bytes": nbytes}
 
 
+def bench_prefill_state(cfg, steps: int):
+    """Prefill -> decode caches for one layer at the C3 shape (4 prompts of 2048 tokens whose current
+    document is the last one of the packed rows, ring of 64), one launch, next to the reference's
+    per-row host loop (reverse_sps/inference.py:568-613) on the same GPU."""
+    import torch
+
+    from sps_amd.prefill_state import prefill_to_decode
+    from sps_amd.workloads import position_doc_ids
+
+    B, T, H, D, W = cfg.batch, cfg.tokens, cfg.heads, cfg.head_dim, cfg.window
+    ids, _ = position_doc_ids(cfg, seed=0)
+    tok = torch.tensor(ids[:, 0::2])
+    mask = (tok == tok[:, -1:]).cuda()
+    g = torch.Generator().manual_seed(0)
+    k = torch.randn(B, 2 * T, H, D, generator=g).cuda()
+    v = torch.randn(B, 2 * T, H, D, generator=g).cuda()
+    z = lambda *sh: torch.zeros(*sh, device="cuda", dtype=torch.bfloat16)  # noqa: E731
+    ring_k, ring_v, ret_k, ret_v = z(B, H, W, D), z(B, H, W, D), z(B, H, T, D), z(B, H, T, D)
+    ring_len = torch.zeros(B, dtype=torch.long, device="cuda")
+    ring_pos = torch.zeros(B, dtype=torch.long, device="cuda")
+    ret_len = torch.zeros(B, H, dtype=torch.long, device="cuda")
+
+    def fused():
+        prefill_to_decode(k, v, mask, window_slot=0, retained_slot=1, nw_k=ring_k, nw_v=ring_v, nw_len=ring_len,
+                          nw_pos=ring_pos, br_k=ret_k, br_v=ret_v, br_len=ret_len, window_tokens=W)
+
+    def reference_loop():
+        kw, vw = k[:, 0::2].to(torch.bfloat16), v[:, 0::2].to(torch.bfloat16)
+        kr, vr = k[:, 1::2].to(torch.bfloat16), v[:, 1::2].to(torch.bfloat16)
+        for b in range(B):
+            pos = mask[b].nonzero(as_tuple=False).flatten()
+            n = int(pos.numel())
+            if n == 0:
+                continue
+            ret_k[b, :, :n, :] = kr[b, pos].transpose(0, 1)
+            ret_v[b, :, :n, :] = vr[b, pos].transpose(0, 1)
+            ret_len[b, :] = n
+            wp = pos[-W:]
+            ring_k[b, :, : wp.numel(), :] = kw[b, wp].transpose(0, 1)
+            ring_v[b, :, : wp.numel(), :] = vw[b, wp].transpose(0, 1)
+            ring_len[b] = wp.numel()
+            ring_pos[b] = 0
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps * 1e6
+
+    us = timed(fused)
+    ref_us = timed(reference_loop)
+    n_doc = int(mask.sum())
+    nbytes = n_doc * H * D * 2 * (4 + 2) + min(W, 1) * B * W * H * D * 2 * (4 + 2)
+    return {"workload": "C3 prefill -> decode caches of one layer (current documents of 4 packed 2048-token rows, "
+                        "ring 64)", "us": round(us, 2), "reference_loop_us": round(ref_us, 2),
+            "document_tokens": n_doc, "algorithmic_bytes": nbytes}
+
+
 def cpu_attention_baseline(cfg, budget_s: float):
     """Reference CPU path (dense masked SDPA fwd + autograd bwd, fp32) on whole batch rows of the same
     inputs until `budget_s` seconds are spent (at least one row)."""
@@ -426,6 +488,8 @@ def main() -> int:
     log(f"C3: {att['value']:.1f} TFLOP/s, {att['ms_per_step']:.3f} ms/step, kernels {att['kernels']}")
     pre = bench_pre_attention(C3, 20)
     log(f"C3 pre-attention (fused RoPE + casts): {pre}")
+    pre["prefill_to_decode"] = bench_prefill_state(C3, 20)
+    log(f"C3 prefill -> decode caches: {pre['prefill_to_decode']}")
     dec = None
     if not args.no_decode:
         log(f"C5 decode: {args.decode_steps} timed steps")

@@ -26,6 +26,8 @@
  *   sps_kv_update                 <- fused_sps_kv_update (utils/decode_attention_fast.py:139-221)
  *   sps_rope_qkv                  <- apply_rotary_emb (model.py:201-230) + the transposes and casts
  *                                    before the attention call (sps/core.py:45-55)
+ *   sps_prefill_to_decode         <- _materialize_prefill_layer_state
+ *                                    (reverse_sps/inference.py:568-613)
  *   sps_attn_mask                 <- the mask block of _attn_fwd_inner_sps
  *                                    (attention/triton_sps_flash_attention.py:70-111); a
  *                                    verification entry point that materialises the mask the
@@ -225,6 +227,28 @@ int sps_rope_qkv(int B, int N, int H, int D, int in_dtype, const void* q, const 
                  const int64_t* freqs_strides, int out_dtype, void* q_out, const int64_t* q_out_strides,
                  void* k_out, const int64_t* k_out_strides, void* v_out, const int64_t* v_out_strides,
                  void* stream);
+
+/*
+ * Prefill -> decode caches of one layer, one launch for the batch (replaces the per-row loop of
+ * _materialize_prefill_layer_state, reverse_sps/inference.py:568-613). k, v: [B, 2T, H, D] of
+ * in_dtype (strides {b, n, h}), the interleaved input/<predict> rows after RoPE; doc_mask: [B, T]
+ * bytes (nonzero: token t belongs to the row's current document; row stride doc_mask_stride).
+ * For every b whose document has n > 0 tokens d_0 < ... < d_{n-1}:
+ *   retained K/V[b, h, j, :] = K/V[b, 2 d_j + retained_slot, h, :] for j < n, ret_len[b, h] = n;
+ *   ring (window_tokens > 0): w = min(n, window_tokens), ring K/V[b, h, i, :] =
+ *     K/V[b, 2 d_{n-w+i} + window_slot, h, :] for i < w, ring_len[b] = w, ring_pos[b] = 0;
+ * other cache rows are untouched, and rows with n == 0 are untouched entirely. Values are converted
+ * to kv_dtype (round to nearest even). Caches and length arrays are described as for sps_kv_update;
+ * rows past ret_storage are not written (the caller sizes the retained buffer for the prompt).
+ * Every row start must be 16-byte aligned; D a multiple of 8.
+ */
+int sps_prefill_to_decode(int B, int T, int H, int D, int in_dtype, const void* k, const int64_t* k_strides,
+                          const void* v, const int64_t* v_strides, int window_slot, int retained_slot,
+                          const uint8_t* doc_mask, int64_t doc_mask_stride, int kv_dtype, void* ring_k,
+                          void* ring_v, const int64_t* ring_strides, int ring_storage, int window_tokens,
+                          void* ring_len, void* ring_pos, const int64_t* ring_len_strides, void* ret_k,
+                          void* ret_v, const int64_t* ret_strides, int ret_storage, void* ret_len,
+                          const int64_t* ret_len_strides, int len_dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -5,6 +5,7 @@ Drop-in replacements for the reference's attention entry points:
   decode:             ``KVSegment``, ``triton_segmented_q1_attention``, ``triton_segmented_q2_attention``,
                       ``masked_kv_attention``, ``fused_sps_kv_update`` (KV-cache update)
   pre-attention:      ``apply_rotary_emb``, ``rope_qkv_for_attention`` (RoPE + casts + layout, one launch)
+  prefill -> decode:  ``prefill_to_decode``, ``materialize_prefill_layer_state`` (decode caches, one launch)
   document ids:       ``generate_left_padded_document_idx``
 All compute runs in libsps_attn.so (hand-written HIP kernels); see include/sps_attn.h.
 """
@@ -25,6 +26,7 @@ from .document_idx import (
 )
 from .integration import install_into_modeling
 from .rope import apply_rotary_emb, rope_qkv_for_attention
+from .prefill_state import materialize_prefill_layer_state, prefill_to_decode
 
 __all__ = [
     "sps_sliding_attention",
@@ -42,4 +44,6 @@ __all__ = [
     "install_into_modeling",
     "apply_rotary_emb",
     "rope_qkv_for_attention",
+    "prefill_to_decode",
+    "materialize_prefill_layer_state",
 ]

@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "sps_decode",
     "sps_kv_update",
     "sps_rope_qkv",
+    "sps_prefill_to_decode",
 )
 
 _i32 = C.c_int
@@ -113,6 +114,13 @@ _SIGNATURES = {
         + [_p, _pi64] * 3
         + [_p, _pi64, _i32]
         + [_p, _pi64] * 3
+        + [_p],
+    ),
+    "sps_prefill_to_decode": (
+        _i32,
+        [_i32, _i32, _i32, _i32, _i32, _p, _pi64, _p, _pi64, _i32, _i32, _p, _i64, _i32]
+        + [_p, _p, _pi64, _i32, _i32, _p, _p, _pi64]  # ring
+        + [_p, _p, _pi64, _i32, _p, _pi64, _i32]  # retained, length dtype
         + [_p],
     ),
 }

@@ -559,4 +559,83 @@ int sps_rope_qkv(int B, int N, int H, int D, int in_dtype, const void* q, const 
   return hip_status(sps::launch_rope_qkv(a, static_cast<hipStream_t>(stream)), "rope");
 }
 
+int sps_prefill_to_decode(int B, int T, int H, int D, int in_dtype, const void* k, const int64_t* k_strides,
+                          const void* v, const int64_t* v_strides, int window_slot, int retained_slot,
+                          const uint8_t* doc_mask, int64_t doc_mask_stride, int kv_dtype, void* ring_k,
+                          void* ring_v, const int64_t* ring_strides, int ring_storage, int window_tokens,
+                          void* ring_len, void* ring_pos, const int64_t* ring_len_strides, void* ret_k,
+                          void* ret_v, const int64_t* ret_strides, int ret_storage, void* ret_len,
+                          const int64_t* ret_len_strides, int len_dtype, void* stream) {
+  g_last_error.clear();
+  if (B < 0 || T < 0 || H < 0 || D < 0) return fail(SPS_E_INVALID, "negative size B=%d T=%d H=%d D=%d", B, T, H, D);
+  auto float_type = [](int t) { return t == SPS_DTYPE_BF16 || t == SPS_DTYPE_F16 || t == SPS_DTYPE_F32; };
+  if (!float_type(in_dtype)) return fail(SPS_E_UNSUPPORTED, "K/V dtype code %d not supported", in_dtype);
+  if (!float_type(kv_dtype)) return fail(SPS_E_UNSUPPORTED, "cache dtype code %d not supported", kv_dtype);
+  if (len_dtype != SPS_DTYPE_I32 && len_dtype != SPS_DTYPE_I64)
+    return fail(SPS_E_INVALID, "lengths must be int32 or int64 (dtype code %d)", len_dtype);
+  if (D % 8 != 0 || D > 8 * 256) return fail(SPS_E_UNSUPPORTED, "head_dim %d must be a multiple of 8", D);
+  if ((window_slot != 0 && window_slot != 1) || (retained_slot != 0 && retained_slot != 1))
+    return fail(SPS_E_INVALID, "slot indices must be 0 or 1");
+  if (ret_storage < 0 || ring_storage < 0) return fail(SPS_E_INVALID, "negative cache storage");
+  if ((int64_t)B * T * H * D == 0) return SPS_OK;
+  if (!k || !v || !doc_mask || !ret_k || !ret_v || !ret_len || !k_strides || !v_strides || !ret_strides ||
+      !ret_len_strides)
+    return fail(SPS_E_INVALID, "K/V, mask or retained cache: null pointer");
+  if (window_tokens > 0 && (!ring_k || !ring_v || !ring_len || !ring_pos || !ring_strides || !ring_len_strides))
+    return fail(SPS_E_INVALID, "ring cache: null pointer");
+  if (window_tokens > ring_storage && window_tokens > 0)
+    return fail(SPS_E_INVALID, "window_tokens %d exceeds the ring storage %d", window_tokens, ring_storage);
+  const int64_t in_el = in_dtype == SPS_DTYPE_F32 ? 4 : 2, kv_el = kv_dtype == SPS_DTYPE_F32 ? 4 : 2;
+  auto aligned_rows = [](const void* p, const int64_t* st, int n, int64_t el) {
+    if (!aligned16(p)) return false;
+    for (int i = 0; i < n; ++i)
+      if ((st[i] * el) % 16 != 0) return false;
+    return true;
+  };
+  if (!aligned_rows(k, k_strides, 3, in_el) || !aligned_rows(v, v_strides, 3, in_el))
+    return fail(SPS_E_INVALID, "K/V rows must start 16-byte aligned (base and strides)");
+  if (!aligned_rows(ret_k, ret_strides, 3, kv_el) || !aligned_rows(ret_v, ret_strides + 3, 3, kv_el) ||
+      (window_tokens > 0 &&
+       (!aligned_rows(ring_k, ring_strides, 3, kv_el) || !aligned_rows(ring_v, ring_strides + 3, 3, kv_el))))
+    return fail(SPS_E_INVALID, "cache rows must start 16-byte aligned (base and strides)");
+  sps::PrefillStateArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.B = B;
+  a.T = T;
+  a.H = H;
+  a.D = D;
+  a.in_dtype = in_dtype;
+  a.kv_dtype = kv_dtype;
+  a.k = k;
+  a.v = v;
+  a.k_sb = k_strides[0], a.k_sn = k_strides[1], a.k_sh = k_strides[2];
+  a.v_sb = v_strides[0], a.v_sn = v_strides[1], a.v_sh = v_strides[2];
+  a.window_slot = window_slot;
+  a.retained_slot = retained_slot;
+  a.mask = doc_mask;
+  a.mask_sb = doc_mask_stride;
+  a.window = window_tokens > 0 ? window_tokens : 0;
+  if (a.window > 0) {
+    a.ring_k = ring_k;
+    a.ring_v = ring_v;
+    a.rk_sb = ring_strides[0], a.rk_sh = ring_strides[1], a.rk_st = ring_strides[2];
+    a.rv_sb = ring_strides[3], a.rv_sh = ring_strides[4], a.rv_st = ring_strides[5];
+    a.ring_storage = ring_storage;
+    a.ring_len = ring_len;
+    a.ring_pos = ring_pos;
+    a.ring_len_sb = ring_len_strides[0];
+    a.ring_pos_sb = ring_len_strides[1];
+  }
+  a.ret_k = ret_k;
+  a.ret_v = ret_v;
+  a.tk_sb = ret_strides[0], a.tk_sh = ret_strides[1], a.tk_st = ret_strides[2];
+  a.tv_sb = ret_strides[3], a.tv_sh = ret_strides[4], a.tv_st = ret_strides[5];
+  a.ret_storage = ret_storage;
+  a.ret_len = ret_len;
+  a.ret_len_sb = ret_len_strides[0];
+  a.ret_len_sh = ret_len_strides[1];
+  a.len_i64 = len_dtype == SPS_DTYPE_I64;
+  return hip_status(sps::launch_prefill_state(a, static_cast<hipStream_t>(stream)), "prefill state");
+}
+
 }  // extern "C"

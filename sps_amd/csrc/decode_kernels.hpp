@@ -119,4 +119,31 @@ struct RopeArgs {
 };
 hipError_t launch_rope_qkv(const RopeArgs& a, hipStream_t stream);
 
+// Prefill -> decode caches of one layer (prefill_state.hip).
+struct PrefillStateArgs {
+  int B, T, H, D;
+  int in_dtype, kv_dtype;
+  const void* k;  // [B, 2T, H, D] (strides b, n, h)
+  const void* v;
+  int64_t k_sb, k_sn, k_sh, v_sb, v_sn, v_sh;
+  int window_slot, retained_slot;  // parity of the ring / retained rows in the 2T positions
+  const uint8_t* mask;             // [B, T] current-document tokens (nonzero = member)
+  int64_t mask_sb;
+  void* ring_k;
+  void* ring_v;
+  int64_t rk_sb, rk_sh, rk_st, rv_sb, rv_sh, rv_st;
+  int ring_storage, window;
+  void* ring_len;
+  void* ring_pos;
+  int64_t ring_len_sb, ring_pos_sb;
+  void* ret_k;
+  void* ret_v;
+  int64_t tk_sb, tk_sh, tk_st, tv_sb, tv_sh, tv_st;
+  int ret_storage;
+  void* ret_len;
+  int64_t ret_len_sb, ret_len_sh;
+  int len_i64;
+};
+hipError_t launch_prefill_state(const PrefillStateArgs& a, hipStream_t stream);
+
 }  // namespace sps
