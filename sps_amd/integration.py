@@ -14,6 +14,8 @@ module paths and names:
         (reverse_sps/inference.py:19-23, full_attention_model.py:41)
     modeling.models.utils.decode_attention_fast.fused_sps_kv_update
         (reverse_sps/inference.py:24)
+    ReverseSPSInferenceMixin._materialize_prefill_layer_state
+        (reverse_sps/inference.py:568-613; the SPS and delayed-state models inherit it)
 
 ``install_into_modeling()`` registers modules under the three attention paths and the KV-update
 path whose functions are sps_amd's, and rebinds the names in any of the consumer modules already
@@ -71,6 +73,14 @@ def install_into_modeling(rope: bool = False) -> list[str]:
     by every attention module) to sps_amd's GPU kernel. It is opt-in because the reference also
     runs that function on CPU tensors, which sps_amd does not support."""
     touched = []
+    inf = sys.modules.get("modeling.models.reverse_sps.inference")
+    mixin = getattr(inf, "ReverseSPSInferenceMixin", None) if inf is not None else None
+    if mixin is not None:
+        # Only the batched (GPU) prefill path calls it (reverse_sps/inference.py:518-530, 669).
+        from .prefill_state import materialize_prefill_layer_state
+
+        mixin._materialize_prefill_layer_state = materialize_prefill_layer_state
+        touched.append("modeling.models.reverse_sps.inference.ReverseSPSInferenceMixin")
     if rope:
         from . import rope as _rope
 
