@@ -198,6 +198,34 @@ def test_full_size_c3_heads_against_oracle():
                 torch.testing.assert_close(got[sl].float().cpu(), torch.from_numpy(want).float(), atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("cfg_name,sel", [("C2", [(0, 0), (7, 11)]), ("C4", [(0, 0), (1, 15)])])
+def test_full_size_c2_c4_heads_against_oracle(cfg_name, sel):
+    # The other benchmark configurations at full size: C2 (standard family, B8 H12 T2048, packed
+    # documents) and C4 (SPS w = 4096, D = 128, B2 H16, 4096 positions): the whole batch runs through
+    # the kernels, and selected (batch, head) slices are checked against the oracle, fwd and bwd.
+    from sps_amd import workloads as W
+
+    cfg = getattr(W, cfg_name)
+    ids, _ = W.position_doc_ids(cfg, seed=0)
+    q, k, v, do = W.make_qkv(cfg, seed=0)
+    fam = {"full": N.FAMILY_FULL, "sps": N.FAMILY_SPS, "reverse_sps": N.FAMILY_REVERSE_SPS}[cfg.family]
+    scale = 1.0 / math.sqrt(cfg.head_dim)
+    dev = torch.device("cuda")
+    qg, kg, vg = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+    docs = torch.tensor(ids, device=dev)
+    out = API[cfg.family](qg, kg, vg, scale, cfg.window, docs, None)
+    out.backward(do.to(dev))
+    for bi, hi in sel:
+        mask = M.batch_mask(fam, ids[bi:bi + 1], window=cfg.window)
+        sl = (slice(bi, bi + 1), slice(hi, hi + 1))
+        qn, kn, vn, don = (t[sl].float().numpy() for t in (q, k, v, do))
+        o_ref, _ = A.forward(qn, kn, vn, mask, scale)
+        dq, dk, dv = A.backward(qn, kn, vn, don, mask, scale)
+        torch.testing.assert_close(out[sl].float().cpu(), torch.from_numpy(o_ref).float(), atol=ATOL, rtol=RTOL)
+        for got, want in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
+            torch.testing.assert_close(got[sl].float().cpu(), torch.from_numpy(want).float(), atol=ATOL, rtol=RTOL)
+
+
 @pytest.mark.parametrize("family", ["full", "reverse_sps"])
 def test_no_cross_document_leakage(family):
     # attention/triton/test_document_leakage.py: poison document 2's K/V with NaN; document 1's
