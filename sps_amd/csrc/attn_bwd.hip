@@ -14,14 +14,15 @@
 //     keys: the w-token window):
 //       S = Q K^T, dP = dO V^T (Q, dO rows from LDS; K, V in registers),
 //       dV^T += dO^T P, dK^T += Q^T dS (dO^T, Q^T fragments via ds_read_b64_tr_b16).
-// Both passes consume their tiles in pairs of 32-row blocks (one barrier per pair) through the
-// run_pairs pipeline: buffer loads one pair ahead into registers, double-buffered LDS. dK and dQ are scaled by sm_scale at the
-// end, as in the reference.
+// Both passes consume their tiles in groups of four 32-row blocks (one barrier per group) through
+// the run_groups pipeline: buffer loads one group ahead into registers, double-buffered LDS; with
+// documents the first group's loads leave right after the workgroup's plan is read. dK and dQ are
+// scaled by sm_scale at the end, as in the reference.
 #include "attn_tiles.hpp"
 
 namespace sps {
 
-// Pairs of blocks whose loads are in flight while a pair is computed (run_pairs).
+// Groups of blocks whose loads are in flight while a group is computed (run_groups).
 constexpr int kLook = 1;
 
 // Blocks per barrier (LDS budget: both passes run 2 workgroups per CU, so four 32-row blocks of
@@ -30,7 +31,7 @@ constexpr int kDqGroup = 4;
 constexpr int kDkdvGroup = 4;
 
 template <int D, class E>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8))) void attn_bwd_dq_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
   constexpr int NG = kDqGroup;
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][NG][G::ELEMS];  // [buffer][block of the group]
@@ -40,14 +41,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   const MaskSpec m = a.m;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c32 = lane & 31;
-  int b, h, qt;
-  q_workgroup(a, b, h, qt);
-  const RowView row = row_view(a, b);
-  const int qp = qt * kTile + wave * kBlock + c32;
+  int b, h;
+  TilePlan tp;
+  q_workgroup(a, b, h, tp);
+  const RowView row = row_view(a, b, tp.mono);
+  const int qp = tp.tile * kTile + wave * kBlock + c32;
   const bool qvalid = qp < m.N;
   const int qsafe = qvalid ? qp : 0;
   QState st;
-  q_setup(a, row, qp, s_span, st);
+  int run_start;
+  const bool planned = q_begin(a, tp, row, qp, s_span, st, run_start);
   const QPlan& plan = st.plan;
   const int nb = plan.count();
   const bool exact = row.mono;
@@ -59,39 +62,23 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   const auto k_off = TileRegs<D>::offsets(tid, (uint32_t)(step * a.sk.n * 2));
   const auto v_off = TileRegs<D>::offsets(tid, (uint32_t)(step * a.sv.n * 2));
 
-  // Q and dO fragments (B operands; lane: query c32, d = 16c + 8g .. +7) and Delta.
-  u32x4_t qf[D / 16], dof[D / 16];
-  float delta;
+  // Q, dO and O fragments (B operands; lane: query c32, d = 16c + 8g .. +7) and the LSE, loaded
+  // raw here; everything computed from them waits until the first group's loads are issued too.
+  u32x4_t qf[D / 16], dof[D / 16], of[D / 16];
+  const int64_t rowid = ((int64_t)b * a.H + h) * m.N + qsafe;
   {
     const uint16_t* qrow = a.q + b * a.sq.b + h * a.sq.h + (int64_t)qsafe * a.sq.n;
     const uint16_t* dorow = a.dO + b * a.sdo.b + h * a.sdo.h + (int64_t)qsafe * a.sdo.n;
     const uint16_t* orow = a.o + b * a.so.b + h * a.so.h + (int64_t)qsafe * a.so.n;
-    float part = 0.f;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
       u32x4_t z = {0u, 0u, 0u, 0u};
       qf[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(qrow + 16 * c + 8 * g) : z;
       dof[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(dorow + 16 * c + 8 * g) : z;
-      const u32x4_t of = qvalid ? *reinterpret_cast<const u32x4_t*>(orow + 16 * c + 8 * g) : z;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        part += E::to_f32((uint16_t)(of[j] & 0xffffu)) * E::to_f32((uint16_t)(dof[c][j] & 0xffffu));
-        part += E::to_f32((uint16_t)(of[j] >> 16)) * E::to_f32((uint16_t)(dof[c][j] >> 16));
-      }
+      of[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(orow + 16 * c + 8 * g) : z;
     }
-    delta = half_sum(part);
   }
-  const int64_t rowid = ((int64_t)b * a.H + h) * m.N + qsafe;
-  if (qvalid && g == 0) a.delta[rowid] = delta;
-  float lse = qvalid ? a.lse[rowid] : 0.f;
-  lse = lse == -INFINITY ? 0.f : lse;  // a query with no visible key: every score is masked to -inf
-
-  // Q pre-scaled by sm_scale * log2(e) (rounded to the input type) and the offsets folded into the
-  // MFMA accumulators: the S tile comes out as S * scale2 - lse and the dP tile as dP - Delta, so
-  // P = exp2(S') and dS = P * dP' cost one VALU operation per element each.
-#pragma unroll
-  for (int c = 0; c < D / 16; ++c) qf[c] = scale_frag<E>(qf[c], a.scale2);
-  const f32x16_t c_s = f32x16_t{} - lse, c_dp = f32x16_t{} - delta;
+  const float lse_raw = qvalid ? a.lse[rowid] : 0.f;
 
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
@@ -132,6 +119,32 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const AttnArgs a) {
   f32x16_t acc[G::DC];
 #pragma unroll
   for (int dc = 0; dc < G::DC; ++dc) acc[dc] = f32x16_t{};
+
+  if (planned) q_lanes(m, qp, run_start, st);
+
+  // Delta = rowsum(O * dO) of the lane's query, stored for the dK/dV pass.
+  float delta;
+  {
+    float part = 0.f;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        part += E::to_f32((uint16_t)(of[c][j] & 0xffffu)) * E::to_f32((uint16_t)(dof[c][j] & 0xffffu));
+        part += E::to_f32((uint16_t)(of[c][j] >> 16)) * E::to_f32((uint16_t)(dof[c][j] >> 16));
+      }
+    }
+    delta = half_sum(part);
+  }
+  if (qvalid && g == 0) a.delta[rowid] = delta;
+  const float lse = lse_raw == -INFINITY ? 0.f : lse_raw;  // a query with no visible key: every score is masked to -inf
+
+  // Q pre-scaled by sm_scale * log2(e) (rounded to the input type) and the offsets folded into the
+  // MFMA accumulators: the S tile comes out as S * scale2 - lse and the dP tile as dP - Delta, so
+  // P = exp2(S') and dS = P * dP' cost one VALU operation per element each.
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) qf[c] = scale_frag<E>(qf[c], a.scale2);
+  const f32x16_t c_s = f32x16_t{} - lse, c_dp = f32x16_t{} - delta;
 
   auto run = [&](auto exact_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
@@ -211,23 +224,25 @@ struct ChunkRegs {
 };
 
 template <int D, class E>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8))) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
   constexpr int NG = kDkdvGroup;
   __shared__ __attribute__((aligned(16))) uint16_t sQ[2][NG][G::ELEMS];  // [buffer][chunk of the group]
   __shared__ __attribute__((aligned(16))) uint16_t sDO[2][NG][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) float sLse[2][NG][kBlock];
-  __shared__ __attribute__((aligned(16))) float sDelta[2][NG][kBlock];
+  __shared__ __attribute__((aligned(16))) float sNegLse[2][NG][kBlock];  // -LSE of the chunk's query rows
+  __shared__ __attribute__((aligned(16))) float sNegDelta[2][NG][kBlock];
   __shared__ int s_span[2 * kWaves];
 
   const MaskSpec m = a.m;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c32 = lane & 31;
-  int b, h, kt;
-  k_workgroup(a, b, h, kt);
-  const RowView row = row_view(a, b);
+  int b, h;
+  TilePlan tp;
+  k_workgroup(a, b, h, tp);
+  const RowView row = row_view(a, b, tp.mono);
   KState st;
-  k_setup(a, row, kt, s_span, st);
+  int run_end;
+  const bool planned = k_begin(a, tp, row, s_span, st, run_end);
   const int kp = st.kp;
   const bool kvalid = st.kvalid;
   const int nc = st.nc;
@@ -253,12 +268,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
       vf[c] = kvalid ? *reinterpret_cast<const u32x4_t*>(vrow + 16 * c + 8 * g) : z;
     }
   }
-  // K pre-scaled by sm_scale * log2(e) (rounded to the input type); the S and dP tiles start from
-  // -LSE and -Delta of their query rows, so they come out of the MFMAs as S * scale2 - LSE and
-  // dP - Delta: P = exp2(S') and dS = P * dP' cost one VALU operation per element each.
-#pragma unroll
-  for (int c = 0; c < D / 16; ++c) kf[c] = scale_frag<E>(kf[c], a.scale2);
-
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
 #pragma unroll
@@ -297,9 +306,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
       rc[slot][y].q.store(sQ[buf][y], tid);
       rc[slot][y].o.store(sDO[buf][y], tid);
       if (tid < kBlock) {
+        // Stored negated: the S and dP accumulators start from these values as they are read.
         const float l = rc[slot][y].lse;
-        sLse[buf][y][tid] = l == -INFINITY ? 0.f : l;  // a query with no visible key: its scores are all masked
-        sDelta[buf][y][tid] = rc[slot][y].delta;
+        sNegLse[buf][y][tid] = l == -INFINITY ? 0.f : -l;  // a query with no visible key: its scores are all masked
+        sNegDelta[buf][y][tid] = -rc[slot][y].delta;
       }
     }
   };
@@ -313,9 +323,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
 
   auto run = [&](auto exact_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
+    // The first group's loads go out with the lanes' run ends and the K/V fragments; what depends
+    // on those waits below, for all of them at once.
+    issue(0, 0);
+    if (planned) k_lanes(m, run_end, st);
+    // K pre-scaled by sm_scale * log2(e) (rounded to the input type); the S and dP tiles start from
+    // -LSE and -Delta of their query rows, so they come out of the MFMAs as S * scale2 - LSE and
+    // dP - Delta: P = exp2(S') and dS = P * dP' cost one VALU operation per element each.
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) kf[c] = scale_frag<E>(kf[c], a.scale2);
     auto cls_of = [&](int i) { return classify_block(st.w, (st.c0 + i) * kBlock, EXACT); };
     const BlockMask bm = build_block_mask(nc, cls_of);
-    run_groups<kLook, NG>(nc, issue, put, [&](int j, int buf) {
+    run_groups<kLook, NG, true>(nc, issue, put, [&](int j, int buf) {
       int act2, full2;
       group_codes<NG>(bm, NG * j, nc, cls_of, act2, full2);
 #pragma unroll
@@ -330,13 +349,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(const AttnArgs a) {
           for (int i4 = 0; i4 < 4; ++i4) {
             // Query rows 8*i4 + 4g + {0..3} of this chunk.
             const f32x4_t l4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                (const SPS_LDS float*)(&sLse[buf][y][8 * i4 + 4 * g]));
+                (const SPS_LDS float*)(&sNegLse[buf][y][8 * i4 + 4 * g]));
             const f32x4_t d4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                (const SPS_LDS float*)(&sDelta[buf][y][8 * i4 + 4 * g]));
+                (const SPS_LDS float*)(&sNegDelta[buf][y][8 * i4 + 4 * g]));
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-              sc[4 * i4 + t] = -l4[t];
-              dp[4 * i4 + t] = -d4[t];
+              sc[4 * i4 + t] = l4[t];
+              dp[4 * i4 + t] = d4[t];
             }
           }
 #pragma unroll
@@ -409,11 +428,13 @@ __global__ __launch_bounds__(256) void mask_dump_kv_kernel(const AttnArgs a) {
   const MaskSpec m = a.m;
   const int tid = threadIdx.x, lane = tid & 63;
   const int g = lane >> 5;
-  int b, h, kt;
-  k_workgroup(a, b, h, kt);
-  const RowView row = row_view(a, b);
+  int b, h;
+  TilePlan tp;
+  k_workgroup(a, b, h, tp);
+  const RowView row = row_view(a, b, tp.mono);
   KState st;
-  k_setup(a, row, kt, s_span, st);
+  int run_end;
+  if (k_begin(a, tp, row, s_span, st, run_end)) k_lanes(m, run_end, st);
   const bool exact = row.mono;
   const int64_t dk_doc = (!exact && st.kvalid) ? load_doc(a, b, st.kp) : 0;
   for (int i = 0; i < st.nc; ++i) {

@@ -8,8 +8,9 @@
 // place.
 //
 // Schedule: the workgroup's key blocks are the union of its lanes' visible intervals (one range of
-// 32-row blocks per key stream, computed once from the prepass's run starts), and each wave
-// classifies each block from four numbers (attn_sched.hpp), so no per-block lookups go to memory.
+// 32-row blocks per key stream; with documents the prepass writes it into the workgroup's plan),
+// and each wave classifies each block from
+// four numbers (attn_sched.hpp), so no per-block lookups go to memory.
 // K/V blocks are consumed in pairs (64 rows, one barrier per pair) through the run_pairs pipeline:
 // buffer loads into registers one pair ahead, double-buffered LDS tiles; rows past the end of the
 // sequence read as zeros.
@@ -40,13 +41,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
   const MaskSpec m = a.m;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c32 = lane & 31;
-  int b, h, qt;
-  q_workgroup(a, b, h, qt);
-  const RowView row = row_view(a, b);
-  const int qp = qt * kTile + wave * kBlock + c32;
+  int b, h;
+  TilePlan tp;
+  q_workgroup(a, b, h, tp);
+  const RowView row = row_view(a, b, tp.mono);
+  const int qp = tp.tile * kTile + wave * kBlock + c32;
   const bool qvalid = qp < m.N;
   QState st;
-  q_setup(a, row, qp, s_span, st);
+  int run_start;
+  const bool planned = q_begin(a, tp, row, qp, s_span, st, run_start);
   const QPlan& plan = st.plan;
   const int nb = plan.count();
   const bool exact = row.mono;
@@ -107,6 +110,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
       rv[slot][y].store(sV[buf][y], tid);
     }
   };
+
+  if (planned) q_lanes(m, qp, run_start, st);
 
   float m_run = -INFINITY, l_run[4] = {0.f, 0.f, 0.f, 0.f};
   f32x16_t acc[G::DC];
@@ -217,13 +222,15 @@ __global__ __launch_bounds__(256) void mask_dump_q_kernel(const AttnArgs a) {
   const MaskSpec m = a.m;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, c32 = lane & 31;
-  int b, h, qt;
-  q_workgroup(a, b, h, qt);
-  const RowView row = row_view(a, b);
-  const int qp = qt * kTile + wave * kBlock + c32;
+  int b, h;
+  TilePlan tp;
+  q_workgroup(a, b, h, tp);
+  const RowView row = row_view(a, b, tp.mono);
+  const int qp = tp.tile * kTile + wave * kBlock + c32;
   const bool qvalid = qp < m.N;
   QState st;
-  q_setup(a, row, qp, s_span, st);
+  int run_start;
+  if (q_begin(a, tp, row, qp, s_span, st, run_start)) q_lanes(m, qp, run_start, st);
   const QPlan& plan = st.plan;
   const bool exact = row.mono;
   const int64_t dq_doc = (!exact && qvalid) ? load_doc(a, b, qp) : 0;

@@ -12,6 +12,22 @@ struct Strides3 {
   int64_t b, h, n;
 };
 
+// Work plan of one workgroup, written by the prepass (when documents are given) in dispatch order,
+// heaviest first, so a workgroup needs one load to start fetching its first tiles.
+struct TilePlan {
+  int tile;    // query tile (forward, dQ) or key tile (dK/dV) of the row
+  int mono;    // 1 when the row's ids are non-decreasing
+  int b0, n0;  // query tile: stream-0 key blocks b0 .. b0 + n0 - 1; key tile: query chunks
+  int b1, n1;  // query tile: temporary-stream key blocks b1 .. b1 + n1 - 1; key tile: unused
+  int pad0, pad1;
+};
+
+// First block and block count of the 32-row blocks covering the index interval [lo, hi] (lo >= 0).
+__host__ __device__ __forceinline__ void cover_blocks(int lo, int hi, int& first, int& count) {
+  first = hi >= lo ? lo / kBlock : 0;
+  count = hi >= lo ? hi / kBlock - first + 1 : 0;
+}
+
 struct AttnArgs {
   const uint16_t* q;
   const uint16_t* k;
@@ -32,8 +48,8 @@ struct AttnArgs {
   int* run_start;  // [B, N] first position of the run of equal ids containing each position
   int* run_end;    // [B, N] last position of that run
   int* row_mono;   // [B] 1 when the row's ids are non-decreasing (runs are the documents)
-  int* q_order;    // [B, q_tiles] query tiles, heaviest first
-  int* k_order;    // [B, k_tiles] key tiles, heaviest first
+  TilePlan* q_plan;  // [B, q_tiles] query-tile plans, heaviest first
+  TilePlan* k_plan;  // [B, k_tiles] key-tile plans, heaviest first
   int B, H;
   float sm_scale;
   float scale2;  // sm_scale * log2(e)
@@ -55,12 +71,13 @@ struct RowView {
   __device__ __forceinline__ int run_end(int p, int N) const { return end ? end[p] : N - 1; }
 };
 
-__device__ __forceinline__ RowView row_view(const AttnArgs& a, int b) {
+// mono < 0: read the row's flag from the prepass output.
+__device__ __forceinline__ RowView row_view(const AttnArgs& a, int b, int mono = -1) {
   RowView r;
   if (a.m.has_docs) {
     r.start = a.run_start + (int64_t)b * a.m.N;
     r.end = a.run_end + (int64_t)b * a.m.N;
-    r.mono = a.row_mono[b] != 0;
+    r.mono = (mono < 0 ? a.row_mono[b] : mono) != 0;
   } else {
     r.start = nullptr;
     r.end = nullptr;
@@ -69,17 +86,19 @@ __device__ __forceinline__ RowView row_view(const AttnArgs& a, int b) {
   return r;
 }
 
-// Query tile processed by workgroup rank `rank` of row b (heaviest first).
-__device__ __forceinline__ int q_tile_of(const AttnArgs& a, int b, int rank) {
+// Plan of workgroup rank `rank` of row b (heaviest first). Without documents no prepass runs: the
+// tile follows the closed-form order (later query tiles see more keys, earlier key tiles are seen
+// by more queries) and the block ranges are left for the kernel to derive (n0 = -1).
+__device__ __forceinline__ TilePlan q_plan_of(const AttnArgs& a, int b, int rank) {
   const int nqt = q_tiles(a.m.N);
-  if (a.m.has_docs) return a.q_order[b * nqt + rank];
-  return nqt - 1 - rank;
+  if (a.m.has_docs) return a.q_plan[(int64_t)b * nqt + rank];
+  return TilePlan{nqt - 1 - rank, 1, 0, -1, 0, 0, 0, 0};
 }
 
-__device__ __forceinline__ int k_tile_of(const AttnArgs& a, int b, int rank) {
+__device__ __forceinline__ TilePlan k_plan_of(const AttnArgs& a, int b, int rank) {
   const int nkt = k_tiles(a.m.family, a.m.N, a.m.P);
-  if (a.m.has_docs) return a.k_order[b * nkt + rank];
-  return rank;
+  if (a.m.has_docs) return a.k_plan[(int64_t)b * nkt + rank];
+  return TilePlan{rank, 1, 0, -1, 0, 0, 0, 0};
 }
 
 // Backward passes (bit mask): kBwdDq computes Delta = rowsum(O * dO) and dQ; kBwdDkdv computes dK and dV

@@ -6,9 +6,11 @@
 // into interval bounds (see attn_sched.hpp). A row with decreasing steps is recorded as one run
 // covering the row (start 0, end N - 1) and the kernels compare ids pair by pair there.
 //
-// It also writes the row's query tiles and key tiles in decreasing order of their (approximate)
-// number of MFMA blocks, so the heaviest workgroups are dispatched first. The order only affects
-// speed: it is always a permutation of the tiles.
+// It also writes the work plan of every query tile and key tile (the 32-row blocks covering the
+// union of the tile's lanes' visible intervals, per stream: exactly what the kernels would derive
+// from the run bounds) in decreasing order of block count, so the heaviest workgroups are
+// dispatched first and each workgroup starts its first tile loads after reading one plan. The order
+// only affects speed: it is always a permutation of the tiles.
 #include "attn_kernels.hpp"
 
 namespace sps {
@@ -17,10 +19,6 @@ constexpr int kPrepThreads = 1024;
 constexpr int kRegIds = 8;  // ids per thread held in registers (rows up to kPrepThreads * kRegIds positions)
 constexpr int kMaxSortTiles = 2048;  // rows with more tiles keep the closed-form order
 constexpr int kLdsRow = kPrepThreads * kRegIds;  // rows up to this length keep their runs in LDS
-
-__device__ __forceinline__ int blocks_in(int lo, int hi) {
-  return hi >= lo ? (hi >> 5) - (lo >> 5) + 1 : 0;
-}
 
 // Run bounds of a position, from the LDS copy (rows up to kLdsRow) or from global memory.
 struct RunBounds {
@@ -32,23 +30,47 @@ struct RunBounds {
   __device__ __forceinline__ int end(int p) const { return e_lds ? e_lds[p] : e_glb[p]; }
 };
 
-// Key blocks of the query tile qt (both streams), from its first and last queries' intervals.
-__device__ int q_tile_cost(const MaskSpec& m, const RunBounds& rb, int qt) {
-  const int qa = qt * kTile, qz = imin(qa + kTile - 1, m.N - 1);
-  Interval a0, a1, z0, z1;
-  query_intervals(m, qa, rb.start(qa), a0, a1);
-  query_intervals(m, qz, rb.start(qz), z0, z1);
-  return blocks_in(imin(a0.lo, z0.lo), imax(a0.hi, z0.hi)) + blocks_in(imin(a1.lo, z1.lo), imax(a1.hi, z1.hi));
+__device__ __forceinline__ int wave_min(int x) { return wave_reduce(x, [](int u, int v) { return imin(u, v); }); }
+__device__ __forceinline__ int wave_max(int x) { return wave_reduce(x, [](int u, int v) { return imax(u, v); }); }
+
+// Plan of query tile qt, computed by one wave (lane l takes queries qa + l and qa + 64 + l): per
+// stream, the blocks covering the union of the queries' key intervals, as q_setup derives it.
+__device__ void q_tile_plan(const MaskSpec& m, const RunBounds& rb, int qt, int& b0, int& n0, int& b1, int& n1) {
+  int lo0 = kEmptyLo, hi0 = kEmptyHi, lo1 = kEmptyLo, hi1 = kEmptyHi;
+  for (int r = threadIdx.x & 63; r < kTile; r += 64) {
+    const int q = qt * kTile + r;
+    if (q < m.N) {
+      Interval i0, i1;
+      query_intervals(m, q, rb.start(q), i0, i1);  // an empty interval is {kEmptyLo, kEmptyHi}
+      lo0 = imin(lo0, i0.lo);
+      hi0 = imax(hi0, i0.hi);
+      lo1 = imin(lo1, i1.lo);
+      hi1 = imax(hi1, i1.hi);
+    }
+  }
+  cover_blocks(wave_min(lo0), wave_max(hi0), b0, n0);
+  cover_blocks(wave_min(lo1), wave_max(hi1), b1, n1);
 }
 
-// Query chunks of the key tile kt, from its first key and the last query of its last key.
-__device__ int k_tile_cost(const MaskSpec& m, const RunBounds& rb, int kt) {
+// Plan of key tile kt, computed by one wave: the query chunks covering the union of its keys'
+// query intervals [k, last query seeing k], as k_setup derives it.
+__device__ void k_tile_plan(const MaskSpec& m, const RunBounds& rb, int kt, int& c0, int& nc) {
   int stream, first;
   k_tile_run(m, kt, stream, first);
   const int len = stream_len(m.family, m.N, stream, m.P);
-  const int last = imin(first + kTile - 1, len - 1);
-  const int k0 = stream_pos(m, stream, first), k1 = stream_pos(m, stream, last);
-  return blocks_in(k0, key_last_query(m, stream, k1, rb.end(k1)));
+  int lo = kEmptyLo, hi = kEmptyHi;
+  for (int r = threadIdx.x & 63; r < kTile; r += 64) {
+    const int t = first + r;
+    if (t < len) {
+      const int kp = stream_pos(m, stream, t);
+      const int last = key_last_query(m, stream, kp, rb.end(kp));
+      if (last >= kp) {
+        lo = imin(lo, kp);
+        hi = imax(hi, last);
+      }
+    }
+  }
+  cover_blocks(wave_min(lo), wave_max(hi), c0, nc);
 }
 
 // Exclusive scan of the per-thread chunk summaries in thread order (reverse: in reverse thread
@@ -76,16 +98,13 @@ __device__ int block_exclusive_scan(int* s, int x, int identity, Op op, bool rev
   return op(carry, ex);
 }
 
-// Writes the order of `n` tiles by decreasing cost (ties: lower index first) into order[0..n),
-// with threads [first, first + count) of the workgroup (rank sort; the cost reads are batched so
-// their LDS latencies overlap).
-__device__ void sort_tiles(const int* cost, int n, int* order, bool ascending_fallback, int first, int count) {
+// Ranks `n` <= kMaxSortTiles tiles by decreasing cost (ties: lower index first) and calls
+// emit(rank, tile) for each, with threads [first, first + count) of the workgroup (rank sort; the
+// cost reads are batched so their LDS latencies overlap).
+template <class Emit>
+__device__ void sort_tiles(const int* cost, int n, int first, int count, Emit emit) {
   const int tid = threadIdx.x - first;
   if (tid < 0 || tid >= count) return;
-  if (n > kMaxSortTiles) {
-    for (int t = tid; t < n; t += count) order[t] = ascending_fallback ? t : n - 1 - t;
-    return;
-  }
   for (int t = tid; t < n; t += count) {
     const int c = cost[t];
     int r = 0, j = 0;
@@ -97,13 +116,14 @@ __device__ void sort_tiles(const int* cost, int n, int* order, bool ascending_fa
       for (int u = 0; u < 8; ++u) r += (x[u] > c) || (x[u] == c && j + u < t);
     }
     for (; j < n; ++j) r += (cost[j] > c) || (cost[j] == c && j < t);
-    order[r] = t;
+    emit(r, t);
   }
 }
 
 __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs a) {
   __shared__ int s_scan[kPrepThreads];
   __shared__ int s_cost[kMaxSortTiles], s_cost_k[kMaxSortTiles];
+  __shared__ int s_qplan[kMaxSortTiles][4], s_kplan[kMaxSortTiles][2];
   __shared__ int s_nonmono;
   __shared__ short s_start[kLdsRow], s_end[kLdsRow];
   const MaskSpec m = a.m;
@@ -202,16 +222,51 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   const bool lds_ok = in_regs;
   const RunBounds rb = {lds_ok ? s_start : nullptr, lds_ok ? s_end : nullptr, start, end};
 
-  // Query-tile and key-tile orders (independent: both cost passes, one barrier, both sorts).
+  // Query-tile and key-tile plans (one wave per tile), then both sorts. Rows with more than
+  // kMaxSortTiles tiles keep the closed-form order (query tiles last to first, key tiles first to
+  // last) and write their plans directly.
   const int nqt = q_tiles(N);
   const int nkt = k_tiles(m.family, N, m.P);
-  if (nqt <= kMaxSortTiles)
-    for (int t = tid; t < nqt; t += kPrepThreads) s_cost[t] = q_tile_cost(m, rb, t);
-  if (nkt <= kMaxSortTiles)
-    for (int t = tid; t < nkt; t += kPrepThreads) s_cost_k[t] = k_tile_cost(m, rb, t);
+  const bool sort_q = nqt <= kMaxSortTiles, sort_k = nkt <= kMaxSortTiles;
+  TilePlan* qplan = a.q_plan + (int64_t)b * nqt;
+  TilePlan* kplan = a.k_plan + (int64_t)b * nkt;
+  const int wave = tid >> 6, mono_flag = mono ? 1 : 0;
+  const bool lead = (tid & 63) == 0;
+  for (int t = wave; t < nqt; t += kPrepWaves) {
+    int b0, n0, b1, n1;
+    q_tile_plan(m, rb, t, b0, n0, b1, n1);
+    if (!lead) continue;
+    if (sort_q) {
+      s_cost[t] = n0 + n1;
+      s_qplan[t][0] = b0;
+      s_qplan[t][1] = n0;
+      s_qplan[t][2] = b1;
+      s_qplan[t][3] = n1;
+    } else {
+      qplan[nqt - 1 - t] = TilePlan{t, mono_flag, b0, n0, b1, n1, 0, 0};
+    }
+  }
+  for (int t = wave; t < nkt; t += kPrepWaves) {
+    int c0, nc;
+    k_tile_plan(m, rb, t, c0, nc);
+    if (!lead) continue;
+    if (sort_k) {
+      s_cost_k[t] = nc;
+      s_kplan[t][0] = c0;
+      s_kplan[t][1] = nc;
+    } else {
+      kplan[t] = TilePlan{t, mono_flag, c0, nc, 0, 0, 0, 0};
+    }
+  }
   __syncthreads();
-  sort_tiles(s_cost, nqt, a.q_order + (int64_t)b * nqt, false, 0, kPrepThreads / 2);
-  sort_tiles(s_cost_k, nkt, a.k_order + (int64_t)b * nkt, true, kPrepThreads / 2, kPrepThreads / 2);
+  if (sort_q)
+    sort_tiles(s_cost, nqt, 0, kPrepThreads / 2, [&](int r, int t) {
+      qplan[r] = TilePlan{t, mono_flag, s_qplan[t][0], s_qplan[t][1], s_qplan[t][2], s_qplan[t][3], 0, 0};
+    });
+  if (sort_k)
+    sort_tiles(s_cost_k, nkt, kPrepThreads / 2, kPrepThreads / 2, [&](int r, int t) {
+      kplan[r] = TilePlan{t, mono_flag, s_kplan[t][0], s_kplan[t][1], 0, 0, 0, 0};
+    });
 }
 
 hipError_t launch_row_layout(const AttnArgs& a, hipStream_t stream) {

@@ -123,11 +123,19 @@ struct WaveSpan {
   int max_lo, min_hi;  // every lane's interval contains [max_lo, min_hi] (lanes with nothing break it)
 };
 
+// Reduction of x over the 64 lanes (all active) with an associative, commutative op; the result is
+// wave-uniform. Inside each row of 16 lanes by DPP moves (VALU, no LDS round trip): quad swaps, then
+// the half-row and row mirrors leave every lane of a row holding the row's result; the four rows
+// are then combined from one lane each.
 template <class Op>
 __device__ __forceinline__ int wave_reduce(int x, Op op) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) x = op(x, __shfl_xor(x, o));
-  return x;
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));   // quad_perm [1, 0, 3, 2]
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));   // quad_perm [2, 3, 0, 1]
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false));  // row_mirror
+  const int r0 = __builtin_amdgcn_readlane(x, 0), r1 = __builtin_amdgcn_readlane(x, 16);
+  const int r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
+  return op(op(r0, r1), op(r2, r3));
 }
 
 __device__ __forceinline__ WaveSpan wave_span(const Interval& r) {

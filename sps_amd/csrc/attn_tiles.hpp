@@ -177,17 +177,22 @@ struct QState {
   QPlan plan;
 };
 
-__device__ __forceinline__ void q_setup(const AttnArgs& a, const RowView& row, int qp, int* s_span, QState& st) {
-  const MaskSpec& m = a.m;
-  const int tid = threadIdx.x, wave = tid >> 6;
+// Lane intervals and wave spans of query qp, whose document run starts at position s.
+__device__ __forceinline__ void q_lanes(const MaskSpec& m, int qp, int s, QState& st) {
   if (qp < m.N) {
-    query_intervals(m, qp, row.run_start(qp), st.r0, st.r1);
+    query_intervals(m, qp, s, st.r0, st.r1);
   } else {
     st.r0 = Interval{kEmptyLo, kEmptyHi};
     st.r1 = st.r0;
   }
   st.w0 = wave_span(st.r0);
   st.w1 = wave_span(st.r1);
+}
+
+// The workgroup's key-block plan: per stream, the 32-row blocks covering the union of its lanes'
+// intervals (one LDS exchange and barrier). The prepass computes the same union for every tile.
+__device__ __forceinline__ void q_plan_from_spans(const MaskSpec& m, int* s_span, QState& st) {
+  const int tid = threadIdx.x, wave = tid >> 6;
   if ((tid & 63) == 0) {
     s_span[4 * wave + 0] = st.w0.min_lo;
     s_span[4 * wave + 1] = st.w0.max_hi;
@@ -205,10 +210,33 @@ __device__ __forceinline__ void q_setup(const AttnArgs& a, const RowView& row, i
   }
   QPlan& p = st.plan;
   p.stream0 = m.family == FAMILY_FULL ? STREAM_NATURAL : STREAM_PERSISTENT;
-  p.b0 = wave_uniform(hi0 >= lo0 ? lo0 / kBlock : 0);
-  p.n0 = wave_uniform(hi0 >= lo0 ? hi0 / kBlock - p.b0 + 1 : 0);
-  p.b1 = wave_uniform(hi1 >= lo1 ? lo1 / kBlock : 0);
-  p.n1 = wave_uniform(hi1 >= lo1 ? hi1 / kBlock - p.b1 + 1 : 0);
+  cover_blocks(lo0, hi0, p.b0, p.n0);
+  cover_blocks(lo1, hi1, p.b1, p.n1);
+  p.b0 = wave_uniform(p.b0);
+  p.n0 = wave_uniform(p.n0);
+  p.b1 = wave_uniform(p.b1);
+  p.n1 = wave_uniform(p.n1);
+}
+
+__device__ __forceinline__ void q_setup(const AttnArgs& a, const RowView& row, int qp, int* s_span, QState& st) {
+  q_lanes(a.m, qp, qp < a.m.N ? row.run_start(qp) : 0, st);
+  q_plan_from_spans(a.m, s_span, st);
+}
+
+// Start of a query-stationary workgroup. With a prepass plan (documents given) the block ranges come
+// from it and the lane's run start is read here; the caller issues its first tile loads and then
+// calls q_lanes(m, qp, run_start, st), so both loads are in flight together. Without a plan (no
+// documents: every run starts at 0, nothing to read) the whole setup runs here.
+__device__ __forceinline__ bool q_begin(const AttnArgs& a, const TilePlan& tp, const RowView& row, int qp,
+                                        int* s_span, QState& st, int& run_start) {
+  run_start = 0;
+  if (tp.n0 < 0) {
+    q_setup(a, row, qp, s_span, st);
+    return false;
+  }
+  st.plan = QPlan{a.m.family == FAMILY_FULL ? STREAM_NATURAL : STREAM_PERSISTENT, tp.b0, tp.n0, tp.b1, tp.n1};
+  if (qp < a.m.N) run_start = row.run_start(qp);
+  return true;
 }
 
 // Workgroup -> (row, head, tile): ranks of the per-row heaviest-first order are outermost, and
@@ -223,12 +251,17 @@ __device__ __forceinline__ int row_rotation(int j, int rank, int H, int BH) {
   return (int)(((int64_t)j + (int64_t)rank * H) % BH);
 }
 
-__device__ __forceinline__ void q_workgroup(const AttnArgs& a, int& b, int& h, int& qt) {
+__device__ __forceinline__ TilePlan uniform_plan(const TilePlan& p) {
+  return TilePlan{wave_uniform(p.tile), wave_uniform(p.mono), wave_uniform(p.b0), wave_uniform(p.n0),
+                  wave_uniform(p.b1),   wave_uniform(p.n1),   0,                  0};
+}
+
+__device__ __forceinline__ void q_workgroup(const AttnArgs& a, int& b, int& h, TilePlan& tp) {
   const int BH = a.B * a.H;
   const int rank = blockIdx.x / BH, bh = row_rotation(blockIdx.x - rank * BH, rank, a.H, BH);
   b = bh / a.H;
   h = bh - b * a.H;
-  qt = q_tile_of(a, b, rank);
+  tp = uniform_plan(q_plan_of(a, b, rank));
 }
 
 
@@ -242,21 +275,30 @@ struct KState {
   int c0, nc;
 };
 
-__device__ __forceinline__ void k_setup(const AttnArgs& a, const RowView& row, int kt, int* s_span, KState& st) {
-  const MaskSpec& m = a.m;
+// The lane's key of key tile kt (lanes 32-63 repeat lanes 0-31).
+__device__ __forceinline__ void k_lane_key(const MaskSpec& m, int kt, KState& st) {
   const int tid = threadIdx.x, wave = tid >> 6, c32 = tid & 31;
   k_tile_run(m, kt, st.stream, st.first);
   const int t = st.first + wave * kBlock + c32;
   st.kvalid = t < stream_len(m.family, m.N, st.stream, m.P);
   st.kp = st.kvalid ? stream_pos(m, st.stream, t) : 0;
+}
+
+// The lane's query interval and the wave span, given the end e of the key's document run.
+__device__ __forceinline__ void k_lanes(const MaskSpec& m, int e, KState& st) {
   if (st.kvalid) {
     st.r.lo = st.kp;
-    st.r.hi = key_last_query(m, st.stream, st.kp, row.run_end(st.kp, m.N));
+    st.r.hi = key_last_query(m, st.stream, st.kp, e);
     if (st.r.hi < st.r.lo) st.r = Interval{kEmptyLo, kEmptyHi};
   } else {
     st.r = Interval{kEmptyLo, kEmptyHi};
   }
   st.w = wave_span(st.r);
+}
+
+// Query chunks covering the union of the workgroup's lane intervals (one LDS exchange and barrier).
+__device__ __forceinline__ void k_plan_from_spans(int* s_span, KState& st) {
+  const int tid = threadIdx.x, wave = tid >> 6;
   if ((tid & 63) == 0) {
     s_span[2 * wave + 0] = st.w.min_lo;
     s_span[2 * wave + 1] = st.w.max_hi;
@@ -268,16 +310,39 @@ __device__ __forceinline__ void k_setup(const AttnArgs& a, const RowView& row, i
     lo = imin(lo, s_span[2 * w + 0]);
     hi = imax(hi, s_span[2 * w + 1]);
   }
-  st.c0 = wave_uniform(hi >= lo ? lo / kBlock : 0);
-  st.nc = wave_uniform(hi >= lo ? hi / kBlock - st.c0 + 1 : 0);
+  cover_blocks(lo, hi, st.c0, st.nc);
+  st.c0 = wave_uniform(st.c0);
+  st.nc = wave_uniform(st.nc);
 }
 
-__device__ __forceinline__ void k_workgroup(const AttnArgs& a, int& b, int& h, int& kt) {
+__device__ __forceinline__ void k_setup(const AttnArgs& a, const RowView& row, int kt, int* s_span, KState& st) {
+  k_lane_key(a.m, kt, st);
+  k_lanes(a.m, st.kvalid ? row.run_end(st.kp, a.m.N) : 0, st);
+  k_plan_from_spans(s_span, st);
+}
+
+// Start of a key-stationary workgroup; as q_begin, with the lane's run end read here and consumed by
+// k_lanes(m, run_end, st) after the caller's first loads are issued.
+__device__ __forceinline__ bool k_begin(const AttnArgs& a, const TilePlan& tp, const RowView& row, int* s_span,
+                                        KState& st, int& run_end) {
+  run_end = 0;
+  if (tp.n0 < 0) {
+    k_setup(a, row, tp.tile, s_span, st);
+    return false;
+  }
+  k_lane_key(a.m, tp.tile, st);
+  st.c0 = tp.b0;
+  st.nc = tp.n0;
+  if (st.kvalid) run_end = row.run_end(st.kp, a.m.N);
+  return true;
+}
+
+__device__ __forceinline__ void k_workgroup(const AttnArgs& a, int& b, int& h, TilePlan& tp) {
   const int BH = a.B * a.H;
   const int rank = blockIdx.x / BH, bh = row_rotation(blockIdx.x - rank * BH, rank, a.H, BH);
   b = bh / a.H;
   h = bh - b * a.H;
-  kt = k_tile_of(a, b, rank);
+  tp = uniform_plan(k_plan_of(a, b, rank));
 }
 
 
@@ -338,13 +403,14 @@ __device__ __forceinline__ void pair_codes(const BlockMask& bm, int i, int nb, C
 // (of L), put(slot, buf) writes a slot to LDS buffer `buf` (0/1), body(j, buf) computes group j
 // from LDS buffer `buf`. Group j + 1 + L is loaded while group j is computed and reaches LDS L
 // iterations later, so each group's loads have L full iterations to land. Unrolled by two, so
-// slots and buffers are compile-time indices. run_pairs is the G = 2 form.
-template <int L, int G = 2, class Issue, class Put, class Body>
+// slots and buffers are compile-time indices. run_pairs is the G = 2 form. kFirstIssued: the
+// caller has already issued group 0 into slot 0 (when nb > 0), ahead of its own setup work.
+template <int L, int G = 2, bool kFirstIssued = false, class Issue, class Put, class Body>
 __device__ __forceinline__ void run_groups(int nb, Issue&& issue, Put&& put, Body&& body) {
   static_assert(L == 1 || L == 2, "lookahead of one or two groups");
   const int np = (nb + G - 1) / G;
   if (np > 0) {
-    issue(0, 0);
+    if (!kFirstIssued) issue(0, 0);
     put(0, 0);
   }
   vmem_wait_all();  // everything loaded before the loop is in registers
@@ -366,9 +432,9 @@ __device__ __forceinline__ void run_groups(int nb, Issue&& issue, Put&& put, Bod
   }
 }
 
-template <int L, class Issue, class Put, class Body>
+template <int L, bool kFirstIssued = false, class Issue, class Put, class Body>
 __device__ __forceinline__ void run_pairs(int nb, Issue&& issue, Put&& put, Body&& body) {
-  run_groups<L, 2>(nb, issue, put, body);
+  run_groups<L, 2, kFirstIssued>(nb, issue, put, body);
 }
 
 // Maximum of the 32 elements of two accumulators as a shallow tree of 3-input maxima (the loops

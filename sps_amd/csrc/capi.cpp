@@ -62,7 +62,7 @@ sps::Strides3 strides(const int64_t* st) {
 bool supported_head_dim(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
 struct AttnLayout {
-  size_t run_start, run_end, row_mono, q_order, k_order, delta, total;
+  size_t run_start, run_end, row_mono, q_plan, k_plan, delta, total;
 };
 
 AttnLayout attn_layout(int family, int B, int H, int N, int has_docs, int backward) {
@@ -78,8 +78,8 @@ AttnLayout attn_layout(int family, int B, int H, int N, int has_docs, int backwa
     l.run_start = take((size_t)B * N * sizeof(int));
     l.run_end = take((size_t)B * N * sizeof(int));
     l.row_mono = take((size_t)B * sizeof(int));
-    l.q_order = take((size_t)B * sps::q_tiles(N) * sizeof(int));
-    l.k_order = take((size_t)B * sps::k_tiles(family, N, P) * sizeof(int));
+    l.q_plan = take((size_t)B * sps::q_tiles(N) * sizeof(sps::TilePlan));
+    l.k_plan = take((size_t)B * sps::k_tiles(family, N, P) * sizeof(sps::TilePlan));
   }
   if (backward) l.delta = take((size_t)B * H * N * sizeof(float));
   l.total = off;
@@ -111,8 +111,8 @@ int setup_common(sps::AttnArgs& a, int family, int B, int H, int N, const void* 
     a.run_start = reinterpret_cast<int*>(ws + l.run_start);
     a.run_end = reinterpret_cast<int*>(ws + l.run_end);
     a.row_mono = reinterpret_cast<int*>(ws + l.row_mono);
-    a.q_order = reinterpret_cast<int*>(ws + l.q_order);
-    a.k_order = reinterpret_cast<int*>(ws + l.k_order);
+    a.q_plan = reinterpret_cast<sps::TilePlan*>(ws + l.q_plan);
+    a.k_plan = reinterpret_cast<sps::TilePlan*>(ws + l.k_plan);
   }
   a.delta = backward ? reinterpret_cast<float*>(ws + l.delta) : nullptr;
   a.B = B;
