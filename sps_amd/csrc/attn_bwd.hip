@@ -136,8 +136,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
     }
     delta = half_sum(part);
   }
-  if (qvalid && g == 0) a.delta[rowid] = delta;
   const float lse = lse_raw == -INFINITY ? 0.f : lse_raw;  // a query with no visible key: every score is masked to -inf
+  if (qvalid && g == 0) {
+    // Seeds of the dK/dV pass for this query: -LSE and -Delta.
+    float* seed = a.seeds + ((int64_t)b * a.H + h) * 2 * m.N + qp;
+    seed[0] = -lse;
+    seed[m.N] = -delta;
+  }
 
   // Q pre-scaled by sm_scale * log2(e) (rounded to the input type) and the offsets folded into the
   // MFMA accumulators: the S tile comes out as S * scale2 - lse and the dP tile as dP - Delta, so
@@ -216,21 +221,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
   }
 }
 
-// Staged query chunk of the dK/dV pass: Q and dO rows plus their LSE and Delta (threads < 32).
+// Register-staged query chunk y of a dK/dV group (head dims below 64): Q and dO rows, plus (in wave
+// y only) the chunk's -LSE (lanes 0-31) or -Delta (lanes 32-63) of query row lane % 32.
 template <int D>
 struct ChunkRegs {
   TileRegs<D> q, o;
-  float lse, delta;
+  uint32_t seed;  // raw bits
 };
 
 template <int D, class E>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8))) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
   constexpr int NG = kDkdvGroup;
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][NG][G::ELEMS];  // [buffer][chunk of the group]
-  __shared__ __attribute__((aligned(16))) uint16_t sDO[2][NG][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) float sNegLse[2][NG][kBlock];  // -LSE of the chunk's query rows
-  __shared__ __attribute__((aligned(16))) float sNegDelta[2][NG][kBlock];
+  // Head dims of 64 and more stage Q / dO chunks and their seeds by direct global -> LDS loads into
+  // dense swizzled tiles; smaller ones through registers into padded tiles.
+  constexpr bool kDma = D >= 64;
+  using DT = DmaTile<kDma ? D : 64>;
+  constexpr int TE = kDma ? DT::ELEMS : G::ELEMS;
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][NG][TE];  // [buffer][chunk of the group]
+  __shared__ __attribute__((aligned(16))) uint16_t sDO[2][NG][TE];
+  // -LSE of the chunk's query rows in [0, kBlock), their -Delta in [kBlock, 2 kBlock).
+  __shared__ __attribute__((aligned(16))) float sSeed[2][NG][2 * kBlock];
   __shared__ int s_span[2 * kWaves];
 
   const MaskSpec m = a.m;
@@ -251,10 +262,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
 
   const BufRsrc q_src = head_rsrc<D>(a.q + b * a.sq.b + h * a.sq.h, a.sq.n, m.N);
   const BufRsrc o_src = head_rsrc<D>(a.dO + b * a.sdo.b + h * a.sdo.h, a.sdo.n, m.N);
-  const auto q_off = TileRegs<D>::offsets(tid, (uint32_t)(a.sq.n * 2));
-  const auto o_off = TileRegs<D>::offsets(tid, (uint32_t)(a.sdo.n * 2));
-  const float* lse_row = a.lse + ((int64_t)b * a.H + h) * m.N;
-  const float* delta_row = a.delta + ((int64_t)b * a.H + h) * m.N;
+  // Seeds of this (row, head): -LSE of every query, then -Delta of every query (written by the dQ pass).
+  const BufRsrc seed_src = make_rsrc(a.seeds + ((int64_t)b * a.H + h) * 2 * m.N, (uint32_t)(2 * m.N * 4));
 
   // K and V fragments: B operands of S = Q K^T and dP = dO V^T (lane: key c32, d = 16c + 8g ..).
   u32x4_t kf[D / 16], vf[D / 16];
@@ -268,12 +277,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
       vf[c] = kvalid ? *reinterpret_cast<const u32x4_t*>(vrow + 16 * c + 8 * g) : z;
     }
   }
+  if constexpr (!kDma) {
 #pragma unroll
-  for (int x = 0; x < 2; ++x) {
+    for (int x = 0; x < 2; ++x) {
 #pragma unroll
-    for (int y = 0; y < NG; ++y) {
-      zero_pad_cols<D>(sQ[x][y], tid);
-      zero_pad_cols<D>(sDO[x][y], tid);
+      for (int y = 0; y < NG; ++y) {
+        zero_pad_cols<D>(sQ[x][y], tid);
+        zero_pad_cols<D>(sDO[x][y], tid);
+      }
     }
   }
 
@@ -281,37 +292,61 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
   const uint32_t q_blk = (uint32_t)(kBlock * a.sq.n * 2), o_blk = (uint32_t)(kBlock * a.sdo.n * 2);
   const uint32_t q_c0 = (uint32_t)((int64_t)st.c0 * kBlock * a.sq.n * 2);
   const uint32_t o_c0 = (uint32_t)((int64_t)st.c0 * kBlock * a.sdo.n * 2);
+  // Byte offset, within the seed buffer, of the seed lane `lane` stages for chunk i (wave y of the
+  // group stages chunk y's): -LSE for lanes 0-31, -Delta for lanes 32-63, of query row lane % 32.
+  auto seed_off = [&](int i) {
+    return (uint32_t)(((lane >> 5) * m.N + imin((st.c0 + i) * kBlock + c32, m.N - 1)) * 4);
+  };
 
+  // Register staging (head dims below 64).
   ChunkRegs<D> rc[kLook][NG];
-  auto issue = [&](int j, int slot) {
+  const auto q_off = TileRegs<D>::offsets(tid, (uint32_t)(a.sq.n * 2));
+  const auto o_off = TileRegs<D>::offsets(tid, (uint32_t)(a.sdo.n * 2));
+  auto issue_regs = [&](int j, int slot) {
 #pragma unroll
     for (int y = 0; y < NG; ++y) {
       const int i = NG * j + y;
       if (i < nc) {
         rc[slot][y].q.load(q_src, q_c0 + (uint32_t)i * q_blk, q_off, tid);
         rc[slot][y].o.load(o_src, o_c0 + (uint32_t)i * o_blk, o_off, tid);
-        if (tid < kBlock) {
-          const int qp = imin((st.c0 + i) * kBlock + tid, m.N - 1);
-          // Raw values: anything computed from them here would wait for this pair's loads now
-          // instead of when the pair is written to LDS one iteration later.
-          rc[slot][y].lse = lse_row[qp];
-          rc[slot][y].delta = delta_row[qp];
-        }
+        if (wave == y % kWaves) rc[slot][y].seed = __builtin_amdgcn_raw_buffer_load_b32(seed_src, seed_off(i), 0, 0);
       }
     }
   };
-  auto put = [&](int slot, int buf) {
+  auto put_regs = [&](int slot, int buf) {
 #pragma unroll
     for (int y = 0; y < NG; ++y) {
       rc[slot][y].q.store(sQ[buf][y], tid);
       rc[slot][y].o.store(sDO[buf][y], tid);
-      if (tid < kBlock) {
-        // Stored negated: the S and dP accumulators start from these values as they are read.
-        const float l = rc[slot][y].lse;
-        sNegLse[buf][y][tid] = l == -INFINITY ? 0.f : -l;  // a query with no visible key: its scores are all masked
-        sNegDelta[buf][y][tid] = -rc[slot][y].delta;
+      if (wave == y % kWaves) sSeed[buf][y][lane] = __builtin_bit_cast(float, rc[slot][y].seed);
+    }
+  };
+  // LDS-DMA staging (head dims of 64 and more).
+  const auto q_dma = DT::sources(tid, (uint32_t)(a.sq.n * 2));
+  const auto o_dma = DT::sources(tid, (uint32_t)(a.sdo.n * 2));
+  auto issue_dma = [&](int j, int buf) {
+#pragma unroll
+    for (int y = 0; y < NG; ++y) {
+      const int i = NG * j + y;
+      if (i < nc) {
+        DT::load(q_src, q_c0 + (uint32_t)i * q_blk, q_dma, sQ[buf][y], wave);
+        DT::load(o_src, o_c0 + (uint32_t)i * o_blk, o_dma, sDO[buf][y], wave);
+        if (wave == y % kWaves) lds_dma_b32(seed_src, sSeed[buf][y], seed_off(i));
       }
     }
+  };
+  // Fragment reads of a staged chunk tile.
+  auto row_frag = [&](const uint16_t* tile, int c) {
+    if constexpr (kDma)
+      return lds_read_b128(tile + DT::frag(c32, g, c));
+    else
+      return lds_read_b128(tile + c32 * G::RS + 16 * c + 8 * g);
+  };
+  auto tr_frag = [&](const uint16_t* tile, int kh, int dc) {
+    if constexpr (kDma)
+      return DT::frag_tr(tile, 16 * kh, dc, lane);
+    else
+      return lds_frag_tr(tile, G::RS, 16 * kh, 32 * dc, lane);
   };
 
   f32x16_t dk[G::DC], dv[G::DC];
@@ -325,16 +360,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
     constexpr bool EXACT = decltype(exact_tag)::value;
     // The first group's loads go out with the lanes' run ends and the K/V fragments; what depends
     // on those waits below, for all of them at once.
-    issue(0, 0);
+    if constexpr (kDma)
+      issue_dma(0, 0);
+    else
+      issue_regs(0, 0);
     if (planned) k_lanes(m, run_end, st);
     // K pre-scaled by sm_scale * log2(e) (rounded to the input type); the S and dP tiles start from
-    // -LSE and -Delta of their query rows, so they come out of the MFMAs as S * scale2 - LSE and
-    // dP - Delta: P = exp2(S') and dS = P * dP' cost one VALU operation per element each.
+    // the seeds -LSE and -Delta of their query rows, so they come out of the MFMAs as
+    // S * scale2 - LSE and dP - Delta: P = exp2(S') and dS = P * dP' cost one VALU operation per
+    // element each.
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) kf[c] = scale_frag<E>(kf[c], a.scale2);
     auto cls_of = [&](int i) { return classify_block(st.w, (st.c0 + i) * kBlock, EXACT); };
     const BlockMask bm = build_block_mask(nc, cls_of);
-    run_groups<kLook, NG, true>(nc, issue, put, [&](int j, int buf) {
+    auto body = [&](int j, int buf) {
       int act2, full2;
       group_codes<NG>(bm, NG * j, nc, cls_of, act2, full2);
 #pragma unroll
@@ -349,9 +388,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
           for (int i4 = 0; i4 < 4; ++i4) {
             // Query rows 8*i4 + 4g + {0..3} of this chunk.
             const f32x4_t l4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                (const SPS_LDS float*)(&sNegLse[buf][y][8 * i4 + 4 * g]));
+                (const SPS_LDS float*)(&sSeed[buf][y][8 * i4 + 4 * g]));
             const f32x4_t d4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                (const SPS_LDS float*)(&sNegDelta[buf][y][8 * i4 + 4 * g]));
+                (const SPS_LDS float*)(&sSeed[buf][y][kBlock + 8 * i4 + 4 * g]));
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
               sc[4 * i4 + t] = l4[t];
@@ -360,8 +399,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
           }
 #pragma unroll
           for (int c = 0; c < D / 16; ++c) {
-            sc = E::mfma(lds_read_b128(tQ + c32 * G::RS + 16 * c + 8 * g), kf[c], sc);
-            dp = E::mfma(lds_read_b128(tDO + c32 * G::RS + 16 * c + 8 * g), vf[c], dp);
+            sc = E::mfma(row_frag(tQ, c), kf[c], sc);
+            dp = E::mfma(row_frag(tDO, c), vf[c], dp);
           }
           if (!((full2 >> y) & 1))
             mask_partial<EXACT>(sc, st.r, st.w, qc, g,
@@ -387,13 +426,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
             for (int kh = 0; kh < 2; ++kh) {
               const u32x4_t pf = {pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]};
               const u32x4_t df = {dsk[4 * kh], dsk[4 * kh + 1], dsk[4 * kh + 2], dsk[4 * kh + 3]};
-              dv[dc] = E::mfma(lds_frag_tr(tDO, G::RS, 16 * kh, 32 * dc, lane), pf, dv[dc]);
-              dk[dc] = E::mfma(lds_frag_tr(tQ, G::RS, 16 * kh, 32 * dc, lane), df, dk[dc]);
+              dv[dc] = E::mfma(tr_frag(tDO, kh, dc), pf, dv[dc]);
+              dk[dc] = E::mfma(tr_frag(tQ, kh, dc), df, dk[dc]);
             }
           }
         }
       }
-    });
+    };
+    if constexpr (kDma)
+      run_groups_dma<NG, true>(nc, issue_dma, body);
+    else
+      run_groups<kLook, NG, true>(nc, issue_regs, put_regs, body);
   };
   if (exact)
     run(std::true_type{});

@@ -40,7 +40,7 @@ struct AttnArgs {
   uint16_t* dv;
   Strides3 sq, sk, sv, so, sdo, sout, sdq, sdk, sdv;
   float* lse;        // [B, H, N] log2-domain log-sum-exp of the scaled scores
-  float* delta;      // [B, H, N] rowsum(O * dO) (backward)
+  float* seeds;      // [B, H, 2, N] backward: -LSE (0 where LSE = -inf) and -Delta = -rowsum(O * dO)
   const void* docs;  // [B, N] int32 or int64 document ids (unit stride along N), or null
   int docs_i64;
   int64_t docs_sb;

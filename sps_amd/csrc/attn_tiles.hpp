@@ -84,6 +84,57 @@ struct TileRegs {
   }
 };
 
+// Dense LDS tile filled by direct global -> LDS loads (head dims of 64 and more): 32 rows of D
+// elements, no padding. The 16-byte chunk c of row r is stored at chunk c ^ swz(r), with
+// swz(r) = 2 (r % 4) + (r / 4) % 2: the 8 consecutive rows that a fragment load reads in one chunk
+// land in 8 distinct chunk slots, and the 4 rows x 2 chunks of each 16-lane group of a transposed
+// read in 4 distinct chunk pairs, so neither access pattern needs the padding column.
+template <int D>
+struct DmaTile {
+  static_assert(D % 64 == 0, "the swizzle needs at least 8 chunks per row");
+  static constexpr int CPR = D / 8;                  // 16-byte chunks per row
+  static constexpr int ELEMS = kBlock * D;           // one staged tile
+  static constexpr int PASSES = ELEMS / (256 * 8);   // 16-byte pieces per thread (1 for D = 64)
+
+  static __device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+  // Byte offsets, from the tile's first row, of the pieces thread tid loads: piece p fills slot
+  // p * 256 + tid of the tile (row slot / CPR, stored chunk slot % CPR).
+  struct Src {
+    uint32_t o[PASSES];
+  };
+  static __device__ __forceinline__ Src sources(int tid, uint32_t row_step_bytes) {
+    Src s;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int slot = p * 256 + tid, r = slot / CPR, c = (slot % CPR) ^ swz(r);
+      s.o[p] = (uint32_t)r * row_step_bytes + (uint32_t)c * 16u;
+    }
+    return s;
+  }
+
+  // Issues the loads of a tile whose first row is at byte `first` of the buffer (one instruction
+  // per piece and wave, each filling the wave's contiguous 1 KiB of the tile).
+  static __device__ __forceinline__ void load(BufRsrc rs, uint32_t first, const Src& s, uint16_t* tile, int wave) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) lds_dma_b128(rs, tile + (p * 256 + wave * 64) * 8, first + s.o[p]);
+  }
+
+  // Element offset of row c32's chunk 2c + g (row-major fragment: 8 consecutive columns 16c + 8g).
+  static __device__ __forceinline__ int frag(int c32, int g, int c) { return c32 * D + ((2 * c) ^ (g ^ swz(c32))) * 8; }
+
+  // The transposed fragment of lds_frag_tr(tile, row_stride, r0, 32 dc, lane) on this layout
+  // (r0 a multiple of 8, so rows r and r + 8 share a swizzle).
+  static __device__ __forceinline__ u32x4_t frag_tr(const uint16_t* tile, int r0, int dc, int lane) {
+    const int s = lane & 15, grp = lane >> 4;
+    const int row = r0 + 4 * (grp >> 1) + (s >> 2);
+    const int y = (2 * (grp & 1) + ((s & 3) >> 1)) ^ swz(row);
+    const uint16_t* p = tile + row * D + ((4 * dc) ^ y) * 8 + 4 * (s & 1);
+    const u32x2_t lo = lds_read_tr16(p), hi = lds_read_tr16(p + 8 * D);
+    return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+  }
+};
+
 // An 8-element fragment multiplied by `s`, rounded back to the element type.
 template <class E>
 __device__ __forceinline__ u32x4_t scale_frag(u32x4_t f, float s) {
@@ -426,6 +477,31 @@ __device__ __forceinline__ void run_groups(int nb, Issue&& issue, Put&& put, Bod
         if (j + 1 < np) put((u + 1) % L, u ^ 1);
         if (j + 1 + L < np) issue(j + 1 + L, (u + 1) % L);
         body(j, u);
+        __syncthreads();
+      }
+    }
+  }
+}
+
+// Pipeline over groups staged by direct global -> LDS loads: issue(j, buf) loads group j into LDS
+// buffer `buf`. Group j + 1 goes into buffer (j + 1) % 2 while group j is computed from buffer j % 2
+// (that buffer's previous group was finished at the barrier ending iteration j - 1); each wave then
+// waits for its own loads and the barrier publishes the group. kFirstIssued: the caller has already
+// issued group 0 into buffer 0 (when nb > 0).
+template <int G, bool kFirstIssued = false, class Issue, class Body>
+__device__ __forceinline__ void run_groups_dma(int nb, Issue&& issue, Body&& body) {
+  const int np = (nb + G - 1) / G;
+  if (!kFirstIssued && np > 0) issue(0, 0);
+  vmem_wait_all();
+  __syncthreads();
+  for (int j0 = 0; j0 < np; j0 += 2) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = j0 + u;
+      if (j < np) {
+        if (j + 1 < np) issue(j + 1, u ^ 1);
+        body(j, u);
+        vmem_wait_all();
         __syncthreads();
       }
     }

@@ -62,7 +62,7 @@ sps::Strides3 strides(const int64_t* st) {
 bool supported_head_dim(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
 
 struct AttnLayout {
-  size_t run_start, run_end, row_mono, q_plan, k_plan, delta, total;
+  size_t run_start, run_end, row_mono, q_plan, k_plan, seeds, total;
 };
 
 AttnLayout attn_layout(int family, int B, int H, int N, int has_docs, int backward) {
@@ -81,7 +81,7 @@ AttnLayout attn_layout(int family, int B, int H, int N, int has_docs, int backwa
     l.q_plan = take((size_t)B * sps::q_tiles(N) * sizeof(sps::TilePlan));
     l.k_plan = take((size_t)B * sps::k_tiles(family, N, P) * sizeof(sps::TilePlan));
   }
-  if (backward) l.delta = take((size_t)B * H * N * sizeof(float));
+  if (backward) l.seeds = take((size_t)B * H * 2 * N * sizeof(float));
   l.total = off;
   return l;
 }
@@ -114,7 +114,7 @@ int setup_common(sps::AttnArgs& a, int family, int B, int H, int N, const void* 
     a.q_plan = reinterpret_cast<sps::TilePlan*>(ws + l.q_plan);
     a.k_plan = reinterpret_cast<sps::TilePlan*>(ws + l.k_plan);
   }
-  a.delta = backward ? reinterpret_cast<float*>(ws + l.delta) : nullptr;
+  a.seeds = backward ? reinterpret_cast<float*>(ws + l.seeds) : nullptr;
   a.B = B;
   a.H = H;
   a.m.family = family;

@@ -151,6 +151,19 @@ __device__ __forceinline__ u32x4_t buf_load_b128(BufRsrc r, uint32_t offset) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
 }
 
+// Direct global -> LDS loads (buffer_load ... lds): lane l's 16 (or 4) bytes at byte `voffset` of
+// the buffer land at lds + 16 l (4 l), so one instruction fills a contiguous 1 KiB (256 B) block
+// whose wave-uniform base goes to M0. The data never passes through VGPRs; completion is counted by
+// vmcnt, so a wave waits for vmcnt before the barrier that hands the block to the other waves.
+// Offsets past the descriptor's range load zeros, as for register loads.
+__device__ __forceinline__ void lds_dma_b128(BufRsrc r, uint16_t* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (SPS_LDS void*)((SPS_LDS uint16_t*)lds), 16, voffset, 0, 0, 0);
+}
+
+__device__ __forceinline__ void lds_dma_b32(BufRsrc r, float* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (SPS_LDS void*)((SPS_LDS float*)lds), 4, voffset, 0, 0, 0);
+}
+
 // s_waitcnt vmcnt(0): waits for every outstanding vector-memory load of the wave. Placed before a
 // software-pipelined loop so the compiler's wait counting does not fall back to vmcnt(0) inside it
 // for registers loaded before the loop.
