@@ -38,7 +38,7 @@ def _new_strides(t: Tensor):
     return t.stride(0), t.stride(1)
 
 
-def fused_sps_kv_update(
+def kv_update_args(
     *,
     nw_k: Tensor,
     nw_v: Tensor,
@@ -53,8 +53,10 @@ def fused_sps_kv_update(
     v_retained_BxHxD: Tensor,
     active_mask_B: Tensor,
     window_tokens: int,
-) -> None:
-    """One-launch KV update of one decode layer (see the module docstring)."""
+) -> tuple:
+    """Validates the arguments of fused_sps_kv_update and returns the argument tuple of its C-ABI call
+    (``sps_kv_update``) on the current stream; the tuple's last element keeps the tensors it points
+    into alive. A caller that repeats one update on the same buffers may build it once."""
     batch_size, n_head, head_dim = k_retained_BxHxD.shape
     window_tokens = int(window_tokens)
     use_ring = window_tokens > 0
@@ -94,7 +96,7 @@ def fused_sps_kv_update(
                 nw_len.data_ptr(), nw_pos.data_ptr(), N.i64_array((nw_len.stride(0), nw_pos.stride(0))))
     else:
         ring = (None, None, N.i64_array((0,) * 6), 0, 0, None, None, N.i64_array((0, 0)))
-    status = N.lib().sps_kv_update(
+    args = (
         batch_size, n_head, head_dim, _FLOAT_DTYPES[br_k.dtype],
         *ring,
         br_k.data_ptr(), br_v.data_ptr(), N.i64_array(ret_st), br_k.size(2),
@@ -103,4 +105,32 @@ def fused_sps_kv_update(
         active_mask_B.data_ptr(), _FLAG_DTYPES[active_mask_B.dtype], active_mask_B.stride(0),
         torch.cuda.current_stream(br_k.device).cuda_stream,
     )
-    N.check("sps_kv_update", status)
+    return args, tuple(new)
+
+
+def run_kv_update(args: tuple) -> None:
+    """Launches a KV update from kv_update_args' tuple."""
+    N.check("sps_kv_update", N.lib().sps_kv_update(*args[0]))
+
+
+def fused_sps_kv_update(
+    *,
+    nw_k: Tensor,
+    nw_v: Tensor,
+    nw_len: Tensor,
+    nw_pos: Tensor,
+    br_k: Tensor,
+    br_v: Tensor,
+    br_len: Tensor,
+    k_window_BxHxD: Tensor,
+    v_window_BxHxD: Tensor,
+    k_retained_BxHxD: Tensor,
+    v_retained_BxHxD: Tensor,
+    active_mask_B: Tensor,
+    window_tokens: int,
+) -> None:
+    """One-launch KV update of one decode layer (see the module docstring)."""
+    run_kv_update(kv_update_args(
+        nw_k=nw_k, nw_v=nw_v, nw_len=nw_len, nw_pos=nw_pos, br_k=br_k, br_v=br_v, br_len=br_len,
+        k_window_BxHxD=k_window_BxHxD, v_window_BxHxD=v_window_BxHxD, k_retained_BxHxD=k_retained_BxHxD,
+        v_retained_BxHxD=v_retained_BxHxD, active_mask_B=active_mask_B, window_tokens=window_tokens))
