@@ -30,14 +30,26 @@ struct RunBounds {
   __device__ __forceinline__ int end(int p) const { return e_lds ? e_lds[p] : e_glb[p]; }
 };
 
-__device__ __forceinline__ int wave_min(int x) { return wave_reduce(x, [](int u, int v) { return imin(u, v); }); }
-__device__ __forceinline__ int wave_max(int x) { return wave_reduce(x, [](int u, int v) { return imax(u, v); }); }
+// Tile plans are computed by rows of 16 lanes (one DPP row per tile, every tile of the row at once):
+// each lane folds 8 of the tile's 128 positions, then the row reduces with four DPP moves, after
+// which every lane of the row holds the result.
+constexpr int kPlanLanes = 16;
 
-// Plan of query tile qt, computed by one wave (lane l takes queries qa + l and qa + 64 + l): per
-// stream, the blocks covering the union of the queries' key intervals, as q_setup derives it.
+template <class Op>
+__device__ __forceinline__ int row16_reduce(int x, Op op) {
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));   // quad_perm [1, 0, 3, 2]
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));   // quad_perm [2, 3, 0, 1]
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  return op(x, __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false));  // row_mirror
+}
+__device__ __forceinline__ int row_min(int x) { return row16_reduce(x, [](int u, int v) { return imin(u, v); }); }
+__device__ __forceinline__ int row_max(int x) { return row16_reduce(x, [](int u, int v) { return imax(u, v); }); }
+
+// Plan of query tile qt, computed by one 16-lane row (lane l takes queries qa + l, qa + l + 16, ..):
+// per stream, the blocks covering the union of the queries' key intervals, as q_setup derives it.
 __device__ void q_tile_plan(const MaskSpec& m, const RunBounds& rb, int qt, int& b0, int& n0, int& b1, int& n1) {
   int lo0 = kEmptyLo, hi0 = kEmptyHi, lo1 = kEmptyLo, hi1 = kEmptyHi;
-  for (int r = threadIdx.x & 63; r < kTile; r += 64) {
+  for (int r = threadIdx.x % kPlanLanes; r < kTile; r += kPlanLanes) {
     const int q = qt * kTile + r;
     if (q < m.N) {
       Interval i0, i1;
@@ -48,18 +60,18 @@ __device__ void q_tile_plan(const MaskSpec& m, const RunBounds& rb, int qt, int&
       hi1 = imax(hi1, i1.hi);
     }
   }
-  cover_blocks(wave_min(lo0), wave_max(hi0), b0, n0);
-  cover_blocks(wave_min(lo1), wave_max(hi1), b1, n1);
+  cover_blocks(row_min(lo0), row_max(hi0), b0, n0);
+  cover_blocks(row_min(lo1), row_max(hi1), b1, n1);
 }
 
-// Plan of key tile kt, computed by one wave: the query chunks covering the union of its keys'
-// query intervals [k, last query seeing k], as k_setup derives it.
+// Plan of key tile kt, computed by one 16-lane row: the query chunks covering the union of its
+// keys' query intervals [k, last query seeing k], as k_setup derives it.
 __device__ void k_tile_plan(const MaskSpec& m, const RunBounds& rb, int kt, int& c0, int& nc) {
   int stream, first;
   k_tile_run(m, kt, stream, first);
   const int len = stream_len(m.family, m.N, stream, m.P);
   int lo = kEmptyLo, hi = kEmptyHi;
-  for (int r = threadIdx.x & 63; r < kTile; r += 64) {
+  for (int r = threadIdx.x % kPlanLanes; r < kTile; r += kPlanLanes) {
     const int t = first + r;
     if (t < len) {
       const int kp = stream_pos(m, stream, t);
@@ -70,7 +82,7 @@ __device__ void k_tile_plan(const MaskSpec& m, const RunBounds& rb, int kt, int&
       }
     }
   }
-  cover_blocks(wave_min(lo), wave_max(hi), c0, nc);
+  cover_blocks(row_min(lo), row_max(hi), c0, nc);
 }
 
 // Exclusive scan of the per-thread chunk summaries in thread order (reverse: in reverse thread
@@ -174,22 +186,17 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   const bool mono = s_nonmono == 0;
 
   if (mono && in_regs) {
+    // LDS copies only; the global arrays are written from them below with coalesced stores.
     int cur = carry_start;
 #pragma unroll
     for (int j = 0; j < kRegIds; ++j) {
       if (flag[j]) cur = p0 + j;
-      if (p0 + j < p1) {
-        start[p0 + j] = cur;
-        s_start[p0 + j] = (short)cur;
-      }
+      if (p0 + j < p1) s_start[p0 + j] = (short)cur;
     }
     int nxt = carry_next;
 #pragma unroll
     for (int j = kRegIds - 1; j >= 0; --j) {
-      if (p0 + j < p1) {
-        end[p0 + j] = nxt - 1;
-        s_end[p0 + j] = (short)(nxt - 1);
-      }
+      if (p0 + j < p1) s_end[p0 + j] = (short)(nxt - 1);
       if (flag[j]) nxt = p0 + j;
     }
   } else if (mono) {
@@ -208,16 +215,32 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
     }
   } else {
     for (int p = p0; p < p1; ++p) {
-      start[p] = 0;
-      end[p] = N - 1;
       if (in_regs) {
         s_start[p] = 0;
         s_end[p] = (short)(N - 1);
+      } else {
+        start[p] = 0;
+        end[p] = N - 1;
       }
     }
   }
   if (tid == 0) a.row_mono[b] = mono ? 1 : 0;
   __syncthreads();  // start/end of the whole row are visible to every thread below
+  if (in_regs) {
+    // Rows held in LDS: one pass of consecutive positions per thread group, 4 per thread (16-byte
+    // stores) when the row length allows.
+    if ((N & 3) == 0) {
+      for (int p = 4 * tid; p < N; p += 4 * kPrepThreads) {
+        *reinterpret_cast<int4*>(start + p) = make_int4(s_start[p], s_start[p + 1], s_start[p + 2], s_start[p + 3]);
+        *reinterpret_cast<int4*>(end + p) = make_int4(s_end[p], s_end[p + 1], s_end[p + 2], s_end[p + 3]);
+      }
+    } else {
+      for (int p = tid; p < N; p += kPrepThreads) {
+        start[p] = s_start[p];
+        end[p] = s_end[p];
+      }
+    }
+  }
   // Rows that fit read their run bounds from LDS (short: positions < kLdsRow <= 32767).
   const bool lds_ok = in_regs;
   const RunBounds rb = {lds_ok ? s_start : nullptr, lds_ok ? s_end : nullptr, start, end};
@@ -230,32 +253,38 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   const bool sort_q = nqt <= kMaxSortTiles, sort_k = nkt <= kMaxSortTiles;
   TilePlan* qplan = a.q_plan + (int64_t)b * nqt;
   TilePlan* kplan = a.k_plan + (int64_t)b * nkt;
-  const int wave = tid >> 6, mono_flag = mono ? 1 : 0;
-  const bool lead = (tid & 63) == 0;
-  for (int t = wave; t < nqt; t += kPrepWaves) {
-    int b0, n0, b1, n1;
-    q_tile_plan(m, rb, t, b0, n0, b1, n1);
-    if (!lead) continue;
-    if (sort_q) {
-      s_cost[t] = n0 + n1;
-      s_qplan[t][0] = b0;
-      s_qplan[t][1] = n0;
-      s_qplan[t][2] = b1;
-      s_qplan[t][3] = n1;
+  const int mono_flag = mono ? 1 : 0;
+  const bool lead = tid % kPlanLanes == 0;
+  constexpr int kRows = kPrepThreads / kPlanLanes;
+  // Query tiles are units [0, nqt), key tiles units [nqt, nqt + nkt); row tid / 16 takes every
+  // kRows-th unit.
+  for (int u = tid / kPlanLanes; u < nqt + nkt; u += kRows) {
+    if (u < nqt) {
+      const int t = u;
+      int b0, n0, b1, n1;
+      q_tile_plan(m, rb, t, b0, n0, b1, n1);
+      if (!lead) continue;
+      if (sort_q) {
+        s_cost[t] = n0 + n1;
+        s_qplan[t][0] = b0;
+        s_qplan[t][1] = n0;
+        s_qplan[t][2] = b1;
+        s_qplan[t][3] = n1;
+      } else {
+        qplan[nqt - 1 - t] = TilePlan{t, mono_flag, b0, n0, b1, n1, 0, 0};
+      }
     } else {
-      qplan[nqt - 1 - t] = TilePlan{t, mono_flag, b0, n0, b1, n1, 0, 0};
-    }
-  }
-  for (int t = wave; t < nkt; t += kPrepWaves) {
-    int c0, nc;
-    k_tile_plan(m, rb, t, c0, nc);
-    if (!lead) continue;
-    if (sort_k) {
-      s_cost_k[t] = nc;
-      s_kplan[t][0] = c0;
-      s_kplan[t][1] = nc;
-    } else {
-      kplan[t] = TilePlan{t, mono_flag, c0, nc, 0, 0, 0, 0};
+      const int t = u - nqt;
+      int c0, nc;
+      k_tile_plan(m, rb, t, c0, nc);
+      if (!lead) continue;
+      if (sort_k) {
+        s_cost_k[t] = nc;
+        s_kplan[t][0] = c0;
+        s_kplan[t][1] = nc;
+      } else {
+        kplan[t] = TilePlan{t, mono_flag, c0, nc, 0, 0, 0, 0};
+      }
     }
   }
   __syncthreads();
