@@ -115,11 +115,12 @@ def bench_attention(cfg, steps: int, warmup: int):
         o, lse, _, _, _, ws = SA.attention_forward(q, k, v, scale, family, cfg.window, docs, keep_layout=True)
         if record:
             e[1].record()
-        SA.attention_backward(do, q, k, v, o, lse, scale, family, cfg.window, docs,
-                              between_passes=(e[2].record if record else None), layout_workspace=ws)
+        dq, dk, dv = SA.attention_backward(do, q, k, v, o, lse, scale, family, cfg.window, docs,
+                                           between_passes=(e[2].record if record else None), layout_workspace=ws)
         if record:
             e[3].record()
             ev.append(e)
+        return o, dq, dk, dv
 
     for _ in range(warmup):
         step(False)
