@@ -226,6 +226,35 @@ def test_full_size_c2_c4_heads_against_oracle(cfg_name, sel):
             torch.testing.assert_close(got[sl].float().cpu(), torch.from_numpy(want).float(), atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("family", ["sps", "reverse_sps"])
+def test_rows_beyond_the_sorted_tile_limit(family):
+    # 262272 positions: 2049 query tiles and 2050 key tiles, past the 2048 tiles the prepass sorts,
+    # so the plans are written in the closed-form order. Documents of at most 48 tokens make the
+    # attention block-diagonal per document: the whole row runs through the kernels, and a few
+    # documents (first, middle, last) are checked against the oracle on their own slices.
+    n, d, w = 262272, 64, 16
+    rng = np.random.default_rng(11)
+    docs = _packed_docs(rng, 1, n // 2, family, max_len=48)[0]
+    g = torch.Generator().manual_seed(11)
+    q, k, v, do = (torch.randn((1, 1, n, d), generator=g).to(torch.bfloat16) for _ in range(4))
+    dev = torch.device("cuda")
+    qg, kg, vg = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+    out = API[family](qg, kg, vg, 0.125, w, torch.from_numpy(docs[None]).to(dev), None)
+    out.backward(do.to(dev))
+    starts = [0] + [i for i in range(1, n) if docs[i] != docs[i - 1]]
+    ends = starts[1:] + [n]
+    for j in (0, 1, len(starts) // 2, len(starts) - 2, len(starts) - 1):
+        s, e = starts[j], ends[j]
+        mask = M.batch_mask(FAMILY[family], [list(docs[s:e])], window=w)  # positions s.. keep their parity (s even)
+        sl = (slice(0, 1), slice(0, 1), slice(s, e))
+        qn, kn, vn, don = (t[sl].float().numpy() for t in (q, k, v, do))
+        o_ref, _ = A.forward(qn, kn, vn, mask, 0.125)
+        dq, dk, dv = A.backward(qn, kn, vn, don, mask, 0.125)
+        torch.testing.assert_close(out[sl].float().cpu(), torch.from_numpy(o_ref).float(), atol=ATOL, rtol=RTOL)
+        for got, want in ((qg.grad, dq), (kg.grad, dk), (vg.grad, dv)):
+            torch.testing.assert_close(got[sl].float().cpu(), torch.from_numpy(want).float(), atol=ATOL, rtol=RTOL)
+
+
 @pytest.mark.parametrize("family", ["full", "reverse_sps"])
 def test_no_cross_document_leakage(family):
     # attention/triton/test_document_leakage.py: poison document 2's K/V with NaN; document 1's
