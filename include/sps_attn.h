@@ -94,7 +94,7 @@ int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype,
 
 /*
  * Backward attention: given dO, writes dq, dk, dv (same dtype as q). o and lse are the forward
- * outputs. The workspace also holds rowsum(o * dO).
+ * outputs. The workspace also holds, per query, -lse and -Delta (Delta = rowsum(o * dO)).
  */
 int sps_attn_bwd(int family, int B, int H, int N, int D, int dtype,
                  const void* q, const int64_t* q_strides,
@@ -111,10 +111,10 @@ int sps_attn_bwd(int family, int B, int H, int N, int D, int dtype,
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* Passes of the backward (sps_attn_bwd runs SPS_BWD_DQ, then SPS_BWD_DKDV, on one stream). */
-#define SPS_BWD_DQ 1   /* Delta = rowsum(o * dO) into the workspace, and dq
+#define SPS_BWD_DQ 1   /* Delta = rowsum(o * dO), and -lse, -Delta per query into the workspace, and dq
                           (reference: _attn_bwd_preprocess + _sps_bwd_dq_kernel,
                           triton_reverse_sps_flash_attention.py:334-348, triton_sps_flash_attention.py:385-488) */
-#define SPS_BWD_DKDV 2 /* dk, dv from the Delta and document ranges the SPS_BWD_DQ pass left in the workspace
+#define SPS_BWD_DKDV 2 /* dk, dv from the -lse / -Delta and document ranges the SPS_BWD_DQ pass left in the workspace
                           (reference: _sps_bwd_dkdv_kernel, triton_sps_flash_attention.py:272-382) */
 
 #define SPS_BWD_REUSE_LAYOUT 4 /* with SPS_BWD_DQ: the workspace already holds the document row layout
