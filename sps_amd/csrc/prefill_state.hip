@@ -10,9 +10,10 @@
 //     K/V[b, 2 doc[n - w + i] + window_slot, :, :] (i < w), ring_len[b] = w, ring_pos[b] = 0,
 // with the rows converted to the cache dtype (round to nearest even).
 //
-// One workgroup per (head, sequence): the mask row is compacted into an LDS list of positions in
-// chunks (a shuffle scan gives each set position its rank), then groups of D/8 threads copy whole
-// rows with 16-byte pieces.
+// kPfSplit workgroups per (head, sequence): each compacts the mask row into an LDS list of positions
+// in chunks (a shuffle scan gives each set position its rank; the row is a few KB, read from L2 by
+// every split), then copies every kPfSplit-th group of rows with groups of D/8 threads moving
+// 16-byte pieces, so a long document is copied by many workgroups at once.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -25,6 +26,7 @@ namespace {
 
 constexpr int kPfThreads = 256;
 constexpr int kPfChunk = 2048;  // positions compacted per pass
+constexpr int kPfSplit = 8;     // workgroups per (head, sequence)
 
 __device__ __forceinline__ void load8(const void* p, int64_t i, int dtype, float* x) {
   if (dtype == 2) {
@@ -93,7 +95,7 @@ __device__ int block_exclusive_sum(int x, int* s_tot, int& total) {
 __global__ __launch_bounds__(kPfThreads) void prefill_state_kernel(const PrefillStateArgs a) {
   __shared__ int s_pos[kPfChunk];
   __shared__ int s_tot[kPfThreads / 64];
-  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int h = blockIdx.x, b = blockIdx.y, split = blockIdx.z, tid = threadIdx.x;
   const uint8_t* mrow = a.mask + (int64_t)b * a.mask_sb;
 
   // Pass 1: the document's length.
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_state_kernel(const Prefill
       if (mrow[t] != 0) s_pos[rank++] = t;
     __syncthreads();
     if (r_in < rows_per_pass) {
-      for (int r = r_in; r < chunk_total; r += rows_per_pass) {
+      for (int r = r_in + split * rows_per_pass; r < chunk_total; r += rows_per_pass * kPfSplit) {
         const int j = base + r;  // rank of this position in the document
         const int t = s_pos[r];
         float x[8];
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_state_kernel(const Prefill
     base += chunk_total;
     __syncthreads();  // s_pos is rewritten by the next chunk
   }
-  if (tid == 0) {
+  if (tid == 0 && split == 0) {
     const int64_t nl = n < a.ret_storage ? n : a.ret_storage;
     const int64_t off = b * a.ret_len_sb + h * a.ret_len_sh;
     if (a.len_i64) reinterpret_cast<int64_t*>(a.ret_len)[off] = nl;
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_state_kernel(const Prefill
 
 hipError_t launch_prefill_state(const PrefillStateArgs& a, hipStream_t stream) {
   if (a.B == 0 || a.H == 0 || a.T == 0) return hipSuccess;
-  hipLaunchKernelGGL(prefill_state_kernel, dim3(a.H, a.B), dim3(kPfThreads), 0, stream, a);
+  hipLaunchKernelGGL(prefill_state_kernel, dim3(a.H, a.B, kPfSplit), dim3(kPfThreads), 0, stream, a);
   return hipGetLastError();
 }
 
