@@ -236,8 +236,12 @@ __device__ __forceinline__ float wave_max_f(float x) {
 }
 
 // One wave per (query slot, head, batch): merges the chunk partials and the extra keys, normalises
-// and writes fp32. Lanes own chunks for the max / sum reductions (in rounds of 64 chunks); the
-// accumulator pass reads 8 chunk records per batch, lanes over d, so loads are issued together.
+// and writes fp32. Everything that depends only on the chunk list is loaded in one round trip
+// before the max reduction: the extra keys' rows, each lane's chunk maximum and weight sum (lanes own
+// chunks, in rounds of 64), and the accumulator rows of the first kMergeAhead chunks (lanes over d).
+// Chunks beyond those are read 8 records per batch after the max is known.
+constexpr int kMergeAhead = 16;
+
 template <int D, int NQ>
 __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
   constexpr int DPL = (D + 63) / 64;  // output elements per lane
@@ -251,24 +255,57 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
   }
   const float* part = a.part + ((int64_t)(b * a.H + h) * a.n_chunks) * NQ * REC + qi * REC;
 
-  // Extra keys: scores (all lanes hold them after the reduction).
+  // The query slice and the extra keys' rows.
   const int64_t q0 = b * a.q_sb + qi * a.q_ss + h * a.q_sh;
-  float es[kMaxDecodeExtras] = {-INFINITY, -INFINITY};
-  for (int e = 0; e < a.n_extra; ++e) {
-    const int64_t e0 = b * a.e_sb + h * a.e_sh;
-    float d = 0.f;
+  const int64_t e0 = b * a.e_sb + h * a.e_sh;
+  float qd[DPL], ekd[kMaxDecodeExtras][DPL], evd[kMaxDecodeExtras][DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) {
+    const int dd = lane + 64 * i;
+    qd[i] = dd < D ? load_as_f32(a.q, q0 + dd, a.q_dtype) : 0.f;
+  }
+#pragma unroll
+  for (int e = 0; e < kMaxDecodeExtras; ++e) {
 #pragma unroll
     for (int i = 0; i < DPL; ++i) {
       const int dd = lane + 64 * i;
-      if (dd < D) d = fmaf(load_as_f32(a.q, q0 + dd, a.q_dtype), load_as_f32(a.ek[e], e0 + dd, a.e_dtype), d);
+      const bool ld = e < a.n_extra && dd < D;
+      ekd[e][i] = ld ? load_as_f32(a.ek[e], e0 + dd, a.e_dtype) : 0.f;
+      evd[e][i] = ld ? load_as_f32(a.ev[e], e0 + dd, a.e_dtype) : 0.f;
     }
+  }
+  // This lane's chunk of the first round (chunk 0's record for idle lanes: in bounds).
+  const int c0 = lane < total ? live_chunk(a, nc, lane) : -1;
+  const float* r0 = part + (int64_t)(c0 < 0 ? 0 : c0) * NQ * REC;
+  const float m0 = r0[D], l0 = r0[D + 1];
+  // Accumulator rows of the first kMergeAhead chunks.
+  float x[kMergeAhead][DPL];
+#pragma unroll
+  for (int u = 0; u < kMergeAhead; ++u) {
+    const int cu = __shfl(c0, u);
+    const float* ru = part + (int64_t)(cu < 0 ? 0 : cu) * NQ * REC;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+      const int dd = lane + 64 * i;
+      x[u][i] = (u < total && dd < D) ? ru[dd] : 0.f;
+    }
+  }
+
+  // Extra-key scores (all lanes hold them after the reduction).
+  float es[kMaxDecodeExtras] = {-INFINITY, -INFINITY};
+#pragma unroll
+  for (int e = 0; e < kMaxDecodeExtras; ++e) {
+    if (e >= a.n_extra) continue;
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) d = fmaf(qd[i], ekd[e][i], d);
     d = xor_sum<64>(d);
     if ((a.emask[e] >> qi) & 1) es[e] = d * a.scale2;
   }
 
   // Max over chunk maxima and extra scores.
-  float M = fmaxf(es[0], es[1]);
-  for (int k0 = 0; k0 < total; k0 += 64) {
+  float M = fmaxf(fmaxf(es[0], es[1]), c0 >= 0 ? m0 : -INFINITY);
+  for (int k0 = 64; k0 < total; k0 += 64) {
     const int c = k0 + lane < total ? live_chunk(a, nc, k0 + lane) : -1;
     const float mc = part[(int64_t)(c < 0 ? 0 : c) * NQ * REC + D];  // in-bounds even for idle lanes
     M = fmaxf(M, c >= 0 ? mc : -INFINITY);
@@ -276,18 +313,13 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
   M = wave_max_f<64>(M);
   const float mu = M == -INFINITY ? 0.f : M;
 
-  // Sum of weights and the weighted accumulators.
+  // Sum of weights and the weighted accumulators, chunk by chunk in order.
   float L = 0.f, A[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; ++i) A[i] = 0.f;
-  for (int k0 = 0; k0 < total; k0 += 64) {
-    const int c = k0 + lane < total ? live_chunk(a, nc, k0 + lane) : -1;
-    const float* rec = part + (int64_t)(c < 0 ? 0 : c) * NQ * REC;
-    const float mrec = rec[D], lrec = rec[D + 1];  // chunk 0's record for idle lanes: in bounds
-    const float f = c >= 0 ? fast_exp2(mrec - mu) : 0.f;
-    L += c >= 0 ? f * lrec : 0.f;
-    const int nk = imin_d(64, total - k0);
-    for (int j0 = 0; j0 < nk; j0 += 8) {
+  // Accumulates the chunks [from, nk) of the round whose lane chunk / weight are (c, f).
+  auto accumulate = [&](int c, float f, int from, int nk) {
+    for (int j0 = from; j0 < nk; j0 += 8) {
       float fj[8];
       const float* rj[8];
 #pragma unroll
@@ -297,31 +329,50 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
         const int cj = __shfl(c, j);
         rj[u] = part + (int64_t)cj * NQ * REC;
       }
-      float x[8][DPL];
+      float xr[8][DPL];
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll
         for (int i = 0; i < DPL; ++i) {
           const int dd = lane + 64 * i;
-          x[u][i] = dd < D ? rj[u][dd] : 0.f;
+          xr[u][i] = dd < D ? rj[u][dd] : 0.f;
         }
 #pragma unroll
       for (int u = 0; u < 8; ++u)
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) A[i] = fmaf(fj[u], x[u][i], A[i]);
+        for (int i = 0; i < DPL; ++i) A[i] = fmaf(fj[u], xr[u][i], A[i]);
     }
+  };
+  {
+    const float f0 = c0 >= 0 ? fast_exp2(m0 - mu) : 0.f;
+    L += c0 >= 0 ? f0 * l0 : 0.f;
+    const int nk = imin_d(64, total);
+#pragma unroll
+    for (int u = 0; u < kMergeAhead; ++u) {
+      const float fu = __shfl(f0, u);
+      if (u < nk) {
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) A[i] = fmaf(fu, x[u][i], A[i]);
+      }
+    }
+    accumulate(c0, f0, kMergeAhead, nk);
+  }
+  for (int k0 = 64; k0 < total; k0 += 64) {
+    const int c = k0 + lane < total ? live_chunk(a, nc, k0 + lane) : -1;
+    const float* rec = part + (int64_t)(c < 0 ? 0 : c) * NQ * REC;
+    const float mrec = rec[D], lrec = rec[D + 1];  // chunk 0's record for idle lanes: in bounds
+    const float f = c >= 0 ? fast_exp2(mrec - mu) : 0.f;
+    L += c >= 0 ? f * lrec : 0.f;
+    accumulate(c, f, 0, imin_d(64, total - k0));
   }
   L = xor_sum<64>(L);
-  for (int e = 0; e < a.n_extra; ++e) {
+#pragma unroll
+  for (int e = 0; e < kMaxDecodeExtras; ++e) {
     if (es[e] == -INFINITY) continue;
     const float f = fast_exp2(es[e] - mu);
     L += f;
-    const int64_t e0 = b * a.e_sb + h * a.e_sh;
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) {
-      const int dd = lane + 64 * i;
-      if (dd < D) A[i] = fmaf(f, load_as_f32(a.ev[e], e0 + dd, a.e_dtype), A[i]);
-    }
+    for (int i = 0; i < DPL; ++i) A[i] = fmaf(f, evd[e][i], A[i]);
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   float* orow = a.out + b * a.o_sb + qi * a.o_ss + h * a.o_sh;
