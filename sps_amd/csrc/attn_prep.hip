@@ -49,8 +49,9 @@ __device__ __forceinline__ int row_max(int x) { return row16_reduce(x, [](int u,
 // per stream, the blocks covering the union of the queries' key intervals, as q_setup derives it.
 __device__ void q_tile_plan(const MaskSpec& m, const RunBounds& rb, int qt, int& b0, int& n0, int& b1, int& n1) {
   int lo0 = kEmptyLo, hi0 = kEmptyHi, lo1 = kEmptyLo, hi1 = kEmptyHi;
-  for (int r = threadIdx.x % kPlanLanes; r < kTile; r += kPlanLanes) {
-    const int q = qt * kTile + r;
+#pragma unroll
+  for (int k = 0; k < kTile / kPlanLanes; ++k) {  // unrolled: the run-bound reads go out together
+    const int q = qt * kTile + threadIdx.x % kPlanLanes + kPlanLanes * k;
     if (q < m.N) {
       Interval i0, i1;
       query_intervals(m, q, rb.start(q), i0, i1);  // an empty interval is {kEmptyLo, kEmptyHi}
@@ -71,8 +72,9 @@ __device__ void k_tile_plan(const MaskSpec& m, const RunBounds& rb, int kt, int&
   k_tile_run(m, kt, stream, first);
   const int len = stream_len(m.family, m.N, stream, m.P);
   int lo = kEmptyLo, hi = kEmptyHi;
-  for (int r = threadIdx.x % kPlanLanes; r < kTile; r += kPlanLanes) {
-    const int t = first + r;
+#pragma unroll
+  for (int k = 0; k < kTile / kPlanLanes; ++k) {
+    const int t = first + threadIdx.x % kPlanLanes + kPlanLanes * k;
     if (t < len) {
       const int kp = stream_pos(m, stream, t);
       const int last = key_last_query(m, stream, kp, rb.end(kp));
@@ -85,29 +87,33 @@ __device__ void k_tile_plan(const MaskSpec& m, const RunBounds& rb, int kt, int&
   cover_blocks(row_min(lo), row_max(hi), c0, nc);
 }
 
-// Exclusive scan of the per-thread chunk summaries in thread order (reverse: in reverse thread
-// order) for an associative, commutative op: a shuffle scan inside each wave, then the waves'
-// totals through LDS (two barriers in all).
+// Exclusive scans of the per-thread chunk summaries, both in one pass so their latencies overlap:
+// a max-scan of `up` in thread order and a min-scan of `down` in reverse thread order (a shuffle
+// scan inside each wave, then the waves' totals through LDS; two barriers in all).
 constexpr int kPrepWaves = kPrepThreads / 64;
 
-template <class Op>
-__device__ int block_exclusive_scan(int* s, int x, int identity, Op op, bool reverse) {
+__device__ void block_exclusive_scans(int* s_up, int* s_down, int up, int down, int up_identity, int down_identity,
+                                      int& up_ex, int& down_ex) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int v = x;  // inclusive scan within the wave
+  int u = up, d = down;  // inclusive scans within the wave
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const int y = reverse ? __shfl_down(v, o) : __shfl_up(v, o);
-    if (reverse ? lane + o < 64 : lane >= o) v = op(v, y);
+    const int yu = __shfl_up(u, o), yd = __shfl_down(d, o);
+    if (lane >= o) u = imax(u, yu);
+    if (lane + o < 64) d = imin(d, yd);
   }
-  const int wslot = reverse ? kPrepWaves - 1 - wave : wave;
-  if (reverse ? lane == 0 : lane == 63) s[wslot] = v;
+  if (lane == 63) s_up[wave] = u;
+  if (lane == 0) s_down[kPrepWaves - 1 - wave] = d;
   __syncthreads();
-  int carry = identity;
-  for (int w = 0; w < wslot; ++w) carry = op(carry, s[w]);
-  int ex = reverse ? __shfl_down(v, 1) : __shfl_up(v, 1);
-  if (reverse ? lane == 63 : lane == 0) ex = identity;
-  __syncthreads();  // the wave totals may be overwritten by the next scan
-  return op(carry, ex);
+  int cu = up_identity, cd = down_identity;
+  for (int w = 0; w < wave; ++w) cu = imax(cu, s_up[w]);
+  for (int w = 0; w < kPrepWaves - 1 - wave; ++w) cd = imin(cd, s_down[w]);
+  int eu = __shfl_up(u, 1), ed = __shfl_down(d, 1);
+  if (lane == 0) eu = up_identity;
+  if (lane == 63) ed = down_identity;
+  __syncthreads();  // the wave totals may be overwritten by a later scan
+  up_ex = imax(cu, eu);
+  down_ex = imin(cd, ed);
 }
 
 // Ranks `n` <= kMaxSortTiles tiles by decreasing cost (ties: lower index first) and calls
@@ -181,8 +187,8 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   }
   __syncthreads();
   if (dec) atomicOr(&s_nonmono, 1);
-  const int carry_start = block_exclusive_scan(s_scan, last, -1, [](int x, int y) { return imax(x, y); }, false);
-  const int carry_next = block_exclusive_scan(s_scan, first, N, [](int x, int y) { return imin(x, y); }, true);
+  int carry_start, carry_next;
+  block_exclusive_scans(s_scan, s_scan + kPrepWaves, last, first, -1, N, carry_start, carry_next);
   const bool mono = s_nonmono == 0;
 
   if (mono && in_regs) {
