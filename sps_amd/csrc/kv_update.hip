@@ -69,7 +69,9 @@ __global__ __launch_bounds__(256) void kv_update_vec_kernel(const KvUpdateArgs a
   __shared__ int64_t s_len[kMaxVecHeads];
   __shared__ int64_t s_ring[2];
   const int b = blockIdx.x, tid = threadIdx.x;
-  if (!load_flag(a.active, (int64_t)b * a.active_sb, a.active_bytes)) return;  // whole workgroup
+  // The active flag is loaded with everything else (an inactive sequence's loads are in bounds and
+  // harmless) and tested once those are in flight, before anything is stored.
+  const bool act = load_flag(a.active, (int64_t)b * a.active_sb, a.active_bytes);
   const bool ring = a.window > 0;
   for (int h = tid; h < a.H; h += 256) s_len[h] = load_len(a.ret_len, b * a.ret_len_sb + h * a.ret_len_sh, a.len_i64);
   if (ring && tid == 0) {
@@ -94,7 +96,10 @@ __global__ __launch_bounds__(256) void kv_update_vec_kernel(const KvUpdateArgs a
         val[u] = *reinterpret_cast<const uint4*>(static_cast<const char*>(src) + (b * sb + h * sh) * esz + j * 16);
       }
     }
-    if (base == 0) __syncthreads();  // old lengths in LDS (uniform: every thread takes the first batch)
+    if (base == 0) {
+      if (!act) return;  // whole workgroup
+      __syncthreads();   // old lengths in LDS (uniform: every thread takes the first batch)
+    }
     const int64_t rlen = ring ? s_ring[0] : 0, rpos = ring ? s_ring[1] : 0;
     const int64_t slot = rlen >= a.window ? rpos : rlen;
     const bool ring_write = ring && slot >= 0 && slot < a.ring_storage;
