@@ -16,9 +16,12 @@
 // swizzled tiles (run_groups_dma), below through registers into padded tiles (run_pairs). Rows past
 // the end of the sequence read as zeros.
 //
-// Softmax: exp2 domain with log2(e) folded into the scale; the running max is only raised (and the
-// accumulator rescaled) when a block's max exceeds it by more than 2^8, so P stays <= 256 and most
-// blocks skip the rescale; row sums of P use v_dot2 on the packed 16-bit P the MFMA consumes.
+// Softmax: exp2 domain. Q is pre-scaled by sm_scale * log2(e) (rounded to the input type, as the
+// backward passes do) and the score MFMAs start from -m_run, so they deliver S * scale2 - m_run and
+// P = exp2 of the accumulator costs one VALU operation per element (the forward is VALU-bound at
+// D = 64: this took it from 70 to 67 us at the benchmark shape). The running max is only raised (and
+// the accumulator rescaled) when a block's max exceeds it by more than 2^8, so P stays <= 256 and
+// most blocks skip the rescale; row sums of P use v_dot2 on the packed 16-bit P the MFMA consumes.
 //
 // Reference semantics: _attn_fwd_sps / _attn_fwd_inner_sps (triton_sps_flash_attention.py:26-269),
 // _attn_fwd (triton_reverse_sps_flash_attention.py:242-331, triton_full_flash_attention.py:204-283):
@@ -161,6 +164,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
     if (nb > 0) issue_dma(0, 0);
 
   if (planned) q_lanes(m, qp, run_start, st);
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) qf[c] = scale_frag<E>(qf[c], a.scale2);
+  f32x16_t cm = f32x16_t{};  // -m_run (0 while no score seen): the score MFMAs start from it
 
   float m_run = -INFINITY, l_run[4] = {0.f, 0.f, 0.f, 0.f};
   f32x16_t acc[G::DC];
@@ -185,7 +191,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
 #pragma unroll
       for (int y = 0; y < 2; ++y) {
         const uint16_t* kt = tK(buf, y);
-        sc[y] = E::mfma(row_frag(kt, 0), qf[0], f32x16_t{});
+        sc[y] = E::mfma(row_frag(kt, 0), qf[0], cm);
 #pragma unroll
         for (int c = 1; c < D / 16; ++c) sc[y] = E::mfma(row_frag(kt, c), qf[c], sc[y]);
       }
@@ -204,24 +210,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
           }
         }
       }
-      const float mb = half_max(max32(sc[0], sc[1])) * a.scale2;
-      const bool need = mb > m_run + kRescaleThreshold;
+      // Scores come out as S * scale2 - m_run: the pair's max relative to the running max.
+      const float mb = half_max(max32(sc[0], sc[1]));
+      const bool need = m_run == -INFINITY ? mb > -INFINITY : mb > kRescaleThreshold;
       if (wave_any(need)) {
-        const float alpha = need ? fast_exp2(m_run - mb) : 1.f;
-        m_run = need ? mb : m_run;
+        const float m_new = need ? (m_run == -INFINITY ? mb : m_run + mb) : m_run;
+        const float alpha = need ? fast_exp2(m_run - m_new) : 1.f;
+        const float sh = need ? mb : 0.f;
+        m_run = m_new;
 #pragma unroll
         for (int r = 0; r < 4; ++r) l_run[r] *= alpha;
 #pragma unroll
         for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
+#pragma unroll
+        for (int y = 0; y < 2; ++y) sc[y] -= sh;
+        cm = f32x16_t{} - (m_run == -INFINITY ? 0.f : m_run);
       }
-      const float mu = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
       for (int y = 0; y < 2; ++y) {
         uint32_t pk[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float p0 = fast_exp2(fmaf(sc[y][2 * e], a.scale2, -mu));
-          const float p1 = fast_exp2(fmaf(sc[y][2 * e + 1], a.scale2, -mu));
+          const float p0 = fast_exp2(sc[y][2 * e]);
+          const float p1 = fast_exp2(sc[y][2 * e + 1]);
           pk[e] = E::pack2(p0, p1);
           l_run[e & 3] = E::sum2(pk[e], l_run[e & 3]);  // four independent partial sums
         }
