@@ -513,18 +513,24 @@ __device__ __forceinline__ void run_pairs(int nb, Issue&& issue, Put&& put, Body
   run_groups<L, 2, kFirstIssued>(nb, issue, put, body);
 }
 
-// Maximum of the 32 elements of two accumulators as a shallow tree of 3-input maxima (the loops
-// are latency-bound, so the reduction depth matters more than its instruction count).
+// Maximum of the 32 elements of two accumulators as a shallow tree of gfx950's 3-input IEEE
+// maximum (v_maximum3_f32: NaN-propagating, so unlike fmaxf it needs no quieting of the MFMA
+// results first; the loops are latency-bound, so the reduction depth matters more than its
+// instruction count).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+
 __device__ __forceinline__ float max32(const f32x16_t& s, const f32x16_t& t) {
   float m[11];
 #pragma unroll
-  for (int k = 0; k < 5; ++k) m[k] = fmaxf(fmaxf(s[3 * k], s[3 * k + 1]), s[3 * k + 2]);
+  for (int k = 0; k < 5; ++k) m[k] = max3f(s[3 * k], s[3 * k + 1], s[3 * k + 2]);
 #pragma unroll
-  for (int k = 0; k < 5; ++k) m[5 + k] = fmaxf(fmaxf(t[3 * k], t[3 * k + 1]), t[3 * k + 2]);
-  m[10] = fmaxf(s[15], t[15]);
-  const float x = fmaxf(fmaxf(m[0], m[1]), m[2]), y = fmaxf(fmaxf(m[3], m[4]), m[5]);
-  const float z = fmaxf(fmaxf(m[6], m[7]), m[8]), w = fmaxf(m[9], m[10]);
-  return fmaxf(fmaxf(x, y), fmaxf(z, w));
+  for (int k = 0; k < 5; ++k) m[5 + k] = max3f(t[3 * k], t[3 * k + 1], t[3 * k + 2]);
+  m[10] = __builtin_elementwise_maximum(s[15], t[15]);
+  const float x = max3f(m[0], m[1], m[2]), y = max3f(m[3], m[4], m[5]);
+  const float z = max3f(m[6], m[7], m[8]);
+  return max3f(x, y, max3f(z, m[9], m[10]));
 }
 
 }  // namespace sps

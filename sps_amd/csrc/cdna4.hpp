@@ -119,7 +119,7 @@ __device__ __forceinline__ u32x4_t lds_frag_tr(const uint16_t* tile, int row_str
 __device__ __forceinline__ float half_max(float x) {
   uint32_t u = __builtin_bit_cast(uint32_t, x);
   auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+  return __builtin_elementwise_maximum(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
 }
 
 __device__ __forceinline__ float half_sum(float x) {
