@@ -168,6 +168,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
   for (int c = 0; c < D / 16; ++c) qf[c] = scale_frag<E>(qf[c], a.scale2);
   f32x16_t cm = f32x16_t{};  // -m_run (0 while no score seen): the score MFMAs start from it
 
+  // The pair's max (relative to m_run) must exceed thr to raise m_run: any score while none has been
+  // seen, then the lazy-rescale threshold.
+  float thr = -INFINITY;
   float m_run = -INFINITY, l_run[4] = {0.f, 0.f, 0.f, 0.f};
   f32x16_t acc[G::DC];
 #pragma unroll
@@ -212,12 +215,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
       }
       // Scores come out as S * scale2 - m_run: the pair's max relative to the running max.
       const float mb = half_max(max32(sc[0], sc[1]));
-      const bool need = m_run == -INFINITY ? mb > -INFINITY : mb > kRescaleThreshold;
+      const bool need = mb > thr;
       if (wave_any(need)) {
         const float m_new = need ? (m_run == -INFINITY ? mb : m_run + mb) : m_run;
         const float alpha = need ? fast_exp2(m_run - m_new) : 1.f;
         const float sh = need ? mb : 0.f;
         m_run = m_new;
+        thr = m_run == -INFINITY ? -INFINITY : kRescaleThreshold;
 #pragma unroll
         for (int r = 0; r < 4; ++r) l_run[r] *= alpha;
 #pragma unroll
