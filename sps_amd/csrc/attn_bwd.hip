@@ -246,19 +246,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
   else
     run(std::false_type{});
 
-  if (qvalid) {
-    uint16_t* orow = a.dq + b * a.sdq.b + h * a.sdq.h + (int64_t)qp * a.sdq.n;
-    const float sc = a.sm_scale;
+  uint16_t* orow = a.dq + b * a.sdq.b + h * a.sdq.h + (int64_t)qsafe * a.sdq.n;
+  const float sc = a.sm_scale;
+  auto piece = [&](int dc, int ii) {
+    return u32x2_t{E::pack2(acc[dc][4 * ii] * sc, acc[dc][4 * ii + 1] * sc),
+                   E::pack2(acc[dc][4 * ii + 2] * sc, acc[dc][4 * ii + 3] * sc)};
+  };
+  // Head dims of 64 and more with 16-byte aligned rows: dQ goes through the wave's idle LDS tile so
+  // every global store writes whole rows.
+  bool staged = false;
+  if constexpr (D >= 64) {
+    if (rows16_ok(a.dq, a.sdq)) {
+      store_rows_via_lds<D>(sK[0][wave], lane, orow, qvalid, piece);
+      staged = true;
+    }
+  }
+  if (qvalid && !staged) {
 #pragma unroll
     for (int dc = 0; dc < G::DC; ++dc) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int d0 = 32 * dc + 8 * ii + 4 * g;
-        if (d0 < D) {
-          u32x2_t w = {E::pack2(acc[dc][4 * ii] * sc, acc[dc][4 * ii + 1] * sc),
-                       E::pack2(acc[dc][4 * ii + 2] * sc, acc[dc][4 * ii + 3] * sc)};
-          *reinterpret_cast<u32x2_t*>(orow + d0) = w;
-        }
+        if (d0 < D) *reinterpret_cast<u32x2_t*>(orow + d0) = piece(dc, ii);
       }
     }
   }
@@ -486,22 +495,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
   else
     run(std::false_type{});
 
-  if (kvalid) {
+  const float sc = a.sm_scale;
+  // Pieces of the lane's key row: d = 32 dc + 8 ii + 4 g .. +3 of dK (scaled by sm_scale) and dV.
+  auto piece_k = [&](int dc, int ii) {
+    return u32x2_t{E::pack2(dk[dc][4 * ii] * sc, dk[dc][4 * ii + 1] * sc),
+                   E::pack2(dk[dc][4 * ii + 2] * sc, dk[dc][4 * ii + 3] * sc)};
+  };
+  auto piece_v = [&](int dc, int ii) {
+    return u32x2_t{E::pack2(dv[dc][4 * ii], dv[dc][4 * ii + 1]), E::pack2(dv[dc][4 * ii + 2], dv[dc][4 * ii + 3])};
+  };
+  // With dense tiles and 16-byte aligned output rows the wave's 32 rows go through its own part of
+  // the (now idle) first staging buffer, so every global store writes whole rows (dK/dV -4.6 % at C3).
+  bool staged = false;
+  if constexpr (kDma) {
+    if (rows16_ok(a.dk, a.sdk) && rows16_ok(a.dv, a.sdv)) {
+      uint16_t* krow = a.dk + b * a.sdk.b + h * a.sdk.h + (int64_t)kp * a.sdk.n;
+      uint16_t* vrow = a.dv + b * a.sdv.b + h * a.sdv.h + (int64_t)kp * a.sdv.n;
+      store_rows_via_lds<D>(sQ[0][wave], lane, krow, kvalid, piece_k);
+      store_rows_via_lds<D>(sDO[0][wave], lane, vrow, kvalid, piece_v);
+      staged = true;
+    }
+  }
+  if (!staged && kvalid) {
     uint16_t* dkrow = a.dk + b * a.sdk.b + h * a.sdk.h + (int64_t)kp * a.sdk.n;
     uint16_t* dvrow = a.dv + b * a.sdv.b + h * a.sdv.h + (int64_t)kp * a.sdv.n;
-    const float sc = a.sm_scale;
 #pragma unroll
     for (int dc = 0; dc < G::DC; ++dc) {
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int d0 = 32 * dc + 8 * ii + 4 * g;
         if (d0 < D) {
-          u32x2_t wk = {E::pack2(dk[dc][4 * ii] * sc, dk[dc][4 * ii + 1] * sc),
-                        E::pack2(dk[dc][4 * ii + 2] * sc, dk[dc][4 * ii + 3] * sc)};
-          u32x2_t wv = {E::pack2(dv[dc][4 * ii], dv[dc][4 * ii + 1]),
-                        E::pack2(dv[dc][4 * ii + 2], dv[dc][4 * ii + 3])};
-          *reinterpret_cast<u32x2_t*>(dkrow + d0) = wk;
-          *reinterpret_cast<u32x2_t*>(dvrow + d0) = wv;
+          *reinterpret_cast<u32x2_t*>(dkrow + d0) = piece_k(dc, ii);
+          *reinterpret_cast<u32x2_t*>(dvrow + d0) = piece_v(dc, ii);
         }
       }
     }

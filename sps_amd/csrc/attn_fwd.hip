@@ -264,17 +264,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
   // Epilogue: combine the two halves' partial sums, normalise, store O (lane = query row) and LSE.
   const float l_tot = half_sum((l_run[0] + l_run[1]) + (l_run[2] + l_run[3]));
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  uint16_t* orow = a.out + b * a.sout.b + h * a.sout.h + (int64_t)(qvalid ? qp : 0) * a.sout.n;
+  auto piece = [&](int dc, int ii) {
+    return u32x2_t{E::pack2(acc[dc][4 * ii] * inv, acc[dc][4 * ii + 1] * inv),
+                   E::pack2(acc[dc][4 * ii + 2] * inv, acc[dc][4 * ii + 3] * inv)};
+  };
+  // With dense tiles and 16-byte aligned rows, O goes through the wave's idle LDS tile so every
+  // global store writes whole rows.
+  bool staged = false;
+  if constexpr (kDma) {
+    if (rows16_ok(a.out, a.sout)) {
+      store_rows_via_lds<D>(tK(wave >> 1, wave & 1), lane, orow, qvalid, piece);
+      staged = true;
+    }
+  }
   if (qvalid) {
-    uint16_t* orow = a.out + b * a.sout.b + h * a.sout.h + (int64_t)qp * a.sout.n;
+    if (!staged) {
 #pragma unroll
-    for (int dc = 0; dc < G::DC; ++dc) {
+      for (int dc = 0; dc < G::DC; ++dc) {
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int d0 = 32 * dc + 8 * ii + 4 * g;
-        if (d0 < D) {
-          u32x2_t w = {E::pack2(acc[dc][4 * ii] * inv, acc[dc][4 * ii + 1] * inv),
-                       E::pack2(acc[dc][4 * ii + 2] * inv, acc[dc][4 * ii + 3] * inv)};
-          *reinterpret_cast<u32x2_t*>(orow + d0) = w;
+        for (int ii = 0; ii < 4; ++ii) {
+          const int d0 = 32 * dc + 8 * ii + 4 * g;
+          if (d0 < D) *reinterpret_cast<u32x2_t*>(orow + d0) = piece(dc, ii);
         }
       }
     }

@@ -513,6 +513,47 @@ __device__ __forceinline__ void run_pairs(int nb, Issue&& issue, Put&& put, Body
   run_groups<L, 2, kFirstIssued>(nb, issue, put, body);
 }
 
+// Stores a wave's 32 output rows of D >= 64 elements held in the MFMA accumulator layout (lane:
+// row c32, elements d = 32 dc + 8 ii + 4 g .. +3 as 8-byte pieces from piece(dc, ii)) through the
+// wave's own idle LDS tile (at least 32 * D elements), so that each global store writes 16 bytes and
+// CPR lanes cover a whole row (half the store instructions of the direct 8-byte stores, each
+// covering whole rows instead of a 16-byte piece of 32 rows). `row` is the lane's own row pointer,
+// `valid` whether that row exists; the wave reads back only what it wrote (LDS operations of one
+// wave complete in order), so no barrier is needed.
+template <int D, class PieceFn>
+__device__ __forceinline__ void store_rows_via_lds(uint16_t* tile, int lane, uint16_t* row, bool valid, PieceFn piece) {
+  static_assert(D >= 64 && D % 64 == 0, "the chunk swizzle needs at least 8 chunks per row");
+  constexpr int CPR = D / 8;     // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;  // rows per store instruction
+  const int c32 = lane & 31, g = lane >> 5;
+  // Chunk ch of row r sits at chunk ch ^ (r & 7): the 32 lanes writing one chunk column spread over
+  // the banks.
+#pragma unroll
+  for (int dc = 0; dc < D / 32; ++dc) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int off = c32 * D + ((4 * dc + ii) ^ (c32 & 7)) * 8 + 4 * g;
+      *reinterpret_cast<SPS_LDS u32x2_t*>((SPS_LDS uint16_t*)(tile + off)) = piece(dc, ii);
+    }
+  }
+  const uint64_t rp = reinterpret_cast<uint64_t>(row);
+#pragma unroll
+  for (int k = 0; k < kBlock / RPI; ++k) {
+    const int r = k * RPI + lane / CPR, ch = lane % CPR;
+    const uint64_t rp_r = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(rp >> 32), r) << 32) |
+                          (uint32_t)__shfl((int)(uint32_t)rp, r);
+    const bool v_r = __shfl((int)valid, r) != 0;
+    const u32x4_t x = lds_read_b128(tile + r * D + (ch ^ (r & 7)) * 8);
+    if (v_r) *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(rp_r) + ch * 8) = x;
+  }
+}
+
+// Whether rows of a [B, H, N, D] 16-bit tensor with strides st (elements) starting at p are all
+// 16-byte aligned.
+__device__ __forceinline__ bool rows16_ok(const void* p, const Strides3& st) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && ((st.b | st.h | st.n) & 7) == 0;
+}
+
 // Maximum of the 32 elements of two accumulators as a shallow tree of gfx950's 3-input IEEE
 // maximum (v_maximum3_f32: NaN-propagating, so unlike fmaxf it needs no quieting of the MFMA
 // results first; the loops are latency-bound, so the reduction depth matters more than its
