@@ -28,6 +28,8 @@
  *                                    before the attention call (sps/core.py:45-55)
  *   sps_prefill_to_decode         <- _materialize_prefill_layer_state
  *                                    (reverse_sps/inference.py:568-613)
+ *   sps_document_ids              <- generate_left_padded_document_idx (model.py:70-99) + the
+ *                                    repeat_interleave(2) of reverse_sps/core.py:226
  *   sps_attn_mask                 <- the mask block of _attn_fwd_inner_sps
  *                                    (attention/triton_sps_flash_attention.py:70-111); a
  *                                    verification entry point that materialises the mask the
@@ -80,7 +82,9 @@ size_t sps_attn_workspace_bytes(int family, int B, int H, int N, int has_docs, i
  * lse: [B, H, N] fp32 contiguous, receives the log2-domain log-sum-exp of the scaled scores
  * (m + log2 l), consumed by sps_attn_bwd. docs may be NULL (no document mask).
  * window: temporary-key window in tokens (SPS families). has_pkw/pkw: optional persistent-key
- * window (the reference's persistent_key_window; has_pkw = 0 means None). sm_scale must be > 0.
+ * window (the reference's persistent_key_window; has_pkw = 0 means None). sm_scale may be any value:
+ * the kernels form S * sm_scale * log2(e) in fp32 from the unscaled 16-bit inputs, as the reference
+ * scales its fp32 scores.
  */
 int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype,
                  const void* q, const int64_t* q_strides,
@@ -249,6 +253,21 @@ int sps_prefill_to_decode(int B, int T, int H, int D, int in_dtype, const void* 
                           void* ring_len, void* ring_pos, const int64_t* ring_len_strides, void* ret_k,
                           void* ret_v, const int64_t* ret_strides, int ret_storage, void* ret_len,
                           const int64_t* ret_len_strides, int len_dtype, void* stream);
+
+/*
+ * Document ids of token rows, one launch for the batch (replaces generate_left_padded_document_idx,
+ * model.py:70-99, and the repeat_interleave(2) of the SPS callers, reverse_sps/core.py:218-227).
+ * tokens: [B, T] int32/int64 with row stride tokens_stride_b. A token is real when it differs from
+ * pad_token_id. A real token's id is the row's pad count plus the number of real EOS tokens
+ * (eos_token_id) strictly before it; the i-th pad token's id is i. Each id is written `repeat` (1 or
+ * 2) times: out[b, t * repeat + r], int32/int64 with row stride out_stride_b (repeat = 2 gives the
+ * [B, 2T] ids of the interleaved input/<predict> sequence). Rows must be left padded: bad_rows
+ * (int32 [B], may be null) receives 1 for a row with a pad token after a real token (its ids follow
+ * the same formula; the reference raises ValueError for such input) and 0 otherwise.
+ */
+int sps_document_ids(int B, int T, const void* tokens, int tokens_dtype, int64_t tokens_stride_b,
+                     int64_t eos_token_id, int64_t pad_token_id, int repeat, void* out, int out_dtype,
+                     int64_t out_stride_b, int* bad_rows, void* stream);
 
 #ifdef __cplusplus
 }

@@ -9,6 +9,11 @@ check it against the numpy oracle. Never imported by the product (``sps_amd``).
   test_sps_attention.py:25-73, test_full_flash_attention.py:29-59). The dense SPS forward of the
   reference has no CPU path of its own (src/modeling/models/sps/core.py:63-67), so this is the CPU
   form of that computation the reference ships.
+* ``stepwise_sps_forward``: the reference's CPU inference path for an SPS-family layer
+  (``forward_efficient`` on CPU, src/modeling/models/reverse_sps/inference.py:437-457,766-830, slot
+  roles sps/inference.py:8-12): token by token, each of the two slots' queries attends through
+  ``masked_kv_attention``'s CPU fallback to the window ring, the retained segment and the current
+  token's keys, and then the ring takes the window slot's K/V and the retained segment the other's.
 * ``padded_masked_kv_attention``: the CPU fallback of ``masked_kv_attention``
   (src/modeling/models/utils/decode_attention.py:637-698): every segment is cut to its largest live
   length, segments and the always-visible extra keys are concatenated into one zero-padded K/V
@@ -90,3 +95,36 @@ def mask_from_docs(family: int, docs_row: np.ndarray, window: int) -> torch.Tens
         persistent = (k % 2) == (1 if family == 2 else 0)
         vis &= persistent | ((q // 2 - k // 2) <= window)
     return vis
+
+
+def stepwise_sps_forward(q, k, v, family: int, window: int, attn_dtype=torch.float32):
+    """q, k, v: [B, H, 2T, D] CPU tensors of one document per row (positions 2t input, 2t+1
+    <predict>). Returns the [B, H, 2T, D] fp32 outputs of the token-by-token decode path.
+
+    SPS (family 1): the ring holds the last `window` <predict> K/V (window slot 1) and the retained
+    segment every earlier input K/V (slot 0); reverse-SPS (family 2) swaps the slots. The input
+    query sees ring + retained + the current input key; the <predict> query also the current
+    <predict> key."""
+    b, h, n, d = q.shape
+    t_max = n // 2
+    window_slot, retained_slot = (1, 0) if family == 1 else (0, 1)
+    ring_k = torch.zeros((b, h, max(window, 1), d), dtype=attn_dtype)
+    ring_v = torch.zeros_like(ring_k)
+    ret_k = torch.zeros((b, h, t_max, d), dtype=attn_dtype)
+    ret_v = torch.zeros_like(ret_k)
+    out = torch.zeros((b, h, n, d), dtype=torch.float32)
+    qa, ka, va = (x.to(attn_dtype) for x in (q, k, v))
+    for t in range(t_max):
+        segs = []
+        if window > 0:
+            segs.append((ring_k, ring_v, torch.full((b,), min(t, window), dtype=torch.int64), window))
+        segs.append((ret_k, ret_v, torch.full((b, h), t, dtype=torch.int64), t_max))
+        cur = [(ka[:, :, 2 * t + s], va[:, :, 2 * t + s]) for s in (0, 1)]
+        out[:, :, 2 * t] = padded_masked_kv_attention(qa[:, :, 2 * t], segs, cur[:1], attn_dtype)
+        out[:, :, 2 * t + 1] = padded_masked_kv_attention(qa[:, :, 2 * t + 1], segs, cur, attn_dtype)
+        if window > 0:
+            ring_k[:, :, t % window] = cur[window_slot][0]
+            ring_v[:, :, t % window] = cur[window_slot][1]
+        ret_k[:, :, t] = cur[retained_slot][0]
+        ret_v[:, :, t] = cur[retained_slot][1]
+    return out

@@ -6,7 +6,7 @@ Drop-in replacements for the reference's attention entry points:
                       ``masked_kv_attention``, ``fused_sps_kv_update`` (KV-cache update)
   pre-attention:      ``apply_rotary_emb``, ``rope_qkv_for_attention`` (RoPE + casts + layout, one launch)
   prefill -> decode:  ``prefill_to_decode``, ``materialize_prefill_layer_state`` (decode caches, one launch)
-  document ids:       ``generate_left_padded_document_idx``
+  document ids:       ``document_ids`` (EOS / left-pad rules, interleaved for the SPS families)
 All compute runs in libsps_attn.so (hand-written HIP kernels); see include/sps_attn.h.
 """
 
@@ -18,12 +18,7 @@ from .decode_attention import (
     triton_segmented_q2_attention,
 )
 from .decode_attention_fast import fused_sps_kv_update
-from .document_idx import (
-    compute_left_padded_position_ids,
-    generate_left_padded_document_idx,
-    infer_is_real_tokens,
-    validate_left_padded_tokens,
-)
+from .doc_ids import document_ids, left_padded_document_ids
 from .integration import install_into_modeling
 from .rope import apply_rotary_emb, rope_qkv_for_attention
 from .prefill_state import materialize_prefill_layer_state, prefill_to_decode
@@ -37,10 +32,8 @@ __all__ = [
     "triton_segmented_q2_attention",
     "masked_kv_attention",
     "fused_sps_kv_update",
-    "generate_left_padded_document_idx",
-    "compute_left_padded_position_ids",
-    "infer_is_real_tokens",
-    "validate_left_padded_tokens",
+    "document_ids",
+    "left_padded_document_ids",
     "install_into_modeling",
     "apply_rotary_emb",
     "rope_qkv_for_attention",

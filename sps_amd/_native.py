@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "sps_kv_update",
     "sps_rope_qkv",
     "sps_prefill_to_decode",
+    "sps_document_ids",
 )
 
 _i32 = C.c_int
@@ -123,6 +124,7 @@ _SIGNATURES = {
         + [_p, _p, _pi64, _i32, _p, _pi64, _i32]  # retained, length dtype
         + [_p],
     ),
+    "sps_document_ids": (_i32, [_i32, _i32, _p, _i32, _i64, _i64, _i64, _i32, _p, _i32, _i64, _p, _p]),
 }
 
 _lib = None

@@ -16,7 +16,7 @@ no padding of N to a multiple of 128 (the kernels bounds-check), no ``.contiguou
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -160,38 +160,70 @@ def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, document
     return dq, dk, dv
 
 
-class _Attention(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, k, v, sm_scale, family, window, documents_idx_BxT, persistent_key_window):
-        _validate(q, k, v, family, documents_idx_BxT)
-        needs_grad = any(t.requires_grad for t in (q, k, v))
-        o, lse, qk, kk, vk, ws = attention_forward(
-            q, k, v, sm_scale, family, window, documents_idx_BxT, persistent_key_window, keep_layout=needs_grad
-        )
-        ctx.layout_ws = ws
-        if documents_idx_BxT is not None:
-            ctx.save_for_backward(qk, kk, vk, o, lse, documents_idx_BxT)
-        else:
-            ctx.save_for_backward(qk, kk, vk, o, lse)
-        ctx.sm_scale = float(sm_scale)
-        ctx.family = family
-        ctx.window = int(window)
-        ctx.pkw = persistent_key_window
-        ctx.has_docs = documents_idx_BxT is not None
-        return o
+# The attention as torch.library custom ops, so a torch.compile'd model (the reference trains with
+# torch.compile, scripts/train.py:420-422) traces it as two opaque calls without a graph break. The
+# forward returns its outputs and, when a backward will follow and documents are given, the
+# workspace holding the document row layout; the backward reuses that layout and writes its -LSE /
+# -Delta seeds into the same workspace (declared as mutated).
+@torch.library.custom_op("sps_amd::attention_fwd", mutates_args=())
+def _attention_fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, docs: Optional[torch.Tensor],
+                      sm_scale: float, family: int, window: int, pkw: Optional[int],
+                      keep_layout: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    o, lse, _, _, _, ws = attention_forward(q, k, v, sm_scale, family, window, docs, pkw, keep_layout=keep_layout)
+    if ws is None:
+        ws = torch.empty((0,), dtype=torch.uint8, device=q.device)
+    return o, lse, ws
 
-    @staticmethod
-    def backward(ctx, do):
-        if ctx.has_docs:
-            q, k, v, o, lse, docs = ctx.saved_tensors
-        else:
-            q, k, v, o, lse = ctx.saved_tensors
-            docs = None
-        dq, dk, dv = attention_backward(
-            do, q, k, v, o, lse, ctx.sm_scale, ctx.family, ctx.window, docs, ctx.pkw, layout_workspace=ctx.layout_ws
-        )
-        ctx.layout_ws = None
-        return dq, dk, dv, None, None, None, None, None
+
+@_attention_fwd_op.register_fake
+def _(q, k, v, docs, sm_scale, family, window, pkw, keep_layout):
+    b, h, n, d = q.shape
+    o = q.new_empty((b, n, h, d)).transpose(1, 2)
+    lse = q.new_empty((b, h, n), dtype=torch.float32)
+    nbytes = 0
+    if keep_layout and docs is not None:
+        nbytes = int(N.lib().sps_attn_workspace_bytes(family, int(b), int(h), int(n), 1, 1))
+    return o, lse, q.new_empty((nbytes,), dtype=torch.uint8)
+
+
+@torch.library.custom_op("sps_amd::attention_bwd", mutates_args=("ws",))
+def _attention_bwd_op(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                      lse: torch.Tensor, docs: Optional[torch.Tensor], ws: torch.Tensor, sm_scale: float, family: int,
+                      window: int, pkw: Optional[int]) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
+    return attention_backward(do, q, k, v, o, lse, sm_scale, family, window, docs, pkw,
+                              layout_workspace=ws if ws.numel() > 0 else None)
+
+
+@_attention_bwd_op.register_fake
+def _(do, q, k, v, o, lse, docs, ws, sm_scale, family, window, pkw):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _attention_setup_context(ctx, inputs, output):
+    q, k, v, docs, sm_scale, family, window, pkw, _ = inputs
+    o, lse, ws = output
+    ctx.save_for_backward(q, k, v, o, lse, docs, ws)
+    ctx.params = (float(sm_scale), int(family), int(window), pkw)
+
+
+def _attention_backward(ctx, do, _dlse, _dws):
+    q, k, v, o, lse, docs, ws = ctx.saved_tensors
+    sm_scale, family, window, pkw = ctx.params
+    dq, dk, dv = torch.ops.sps_amd.attention_bwd(do, q, k, v, o, lse, docs, ws, sm_scale, family, window, pkw)
+    return dq, dk, dv, None, None, None, None, None, None
+
+
+_attention_fwd_op.register_autograd(_attention_backward, setup_context=_attention_setup_context)
+
+
+def _attention(q, k, v, sm_scale, family, window, documents_idx_BxT, persistent_key_window):
+    _validate(q, k, v, family, documents_idx_BxT)
+    keep = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
+    o, _, _ = torch.ops.sps_amd.attention_fwd(
+        q, k, v, documents_idx_BxT, float(sm_scale), int(family), int(window),
+        None if persistent_key_window is None else int(persistent_key_window), keep)
+    return o
 
 
 def sps_sliding_attention(
@@ -213,9 +245,7 @@ def sps_sliding_attention(
     equal ids. q, k, v: [B, H, 2T, D] bf16/f16. Reference: triton_sps_flash_attention.py:725-753.
     """
     del warp_specialize
-    return _Attention.apply(
-        q, k, v, sm_scale, N.FAMILY_SPS, temporary_key_window, documents_idx_BxT, persistent_key_window
-    )
+    return _attention(q, k, v, sm_scale, N.FAMILY_SPS, temporary_key_window, documents_idx_BxT, persistent_key_window)
 
 
 def reverse_sps_sliding_attention(
@@ -234,10 +264,8 @@ def reverse_sps_sliding_attention(
     triton_reverse_sps_flash_attention.py:827-853.
     """
     del warp_specialize
-    return _Attention.apply(
-        q, k, v, sm_scale, N.FAMILY_REVERSE_SPS, temporary_key_window, documents_idx_BxT,
-        persistent_key_window,
-    )
+    return _attention(q, k, v, sm_scale, N.FAMILY_REVERSE_SPS, temporary_key_window, documents_idx_BxT,
+                      persistent_key_window)
 
 
 def full_attention(
@@ -254,7 +282,7 @@ def full_attention(
     ``documents_idx_BxT`` is None). Reference: triton_full_flash_attention.py:679-709.
     """
     del warp_specialize
-    return _Attention.apply(q, k, v, sm_scale, N.FAMILY_FULL, 0, documents_idx_BxT, None)
+    return _attention(q, k, v, sm_scale, N.FAMILY_FULL, 0, documents_idx_BxT, None)
 
 
 def attention_mask(family: int, n: int, documents_idx_BxT: Optional[torch.Tensor] = None, *, batch: int = 1,

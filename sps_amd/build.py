@@ -36,7 +36,7 @@ HIP_FLAGS = [
     "-amdgpu-mfma-vgpr-form=1",
 ]
 
-SOURCES = ["attn_prep.hip", "attn_fwd.hip", "attn_bwd.hip", "decode.hip", "kv_update.hip", "rope.hip", "prefill_state.hip", "capi.cpp"]
+SOURCES = ["attn_prep.hip", "attn_fwd.hip", "attn_bwd.hip", "decode.hip", "kv_update.hip", "rope.hip", "prefill_state.hip", "doc_ids.hip", "capi.cpp"]
 
 
 def _hipcc() -> str:

@@ -6,13 +6,15 @@
 //     Delta = rowsum(O * dO) for its own queries and stores it for pass 2 (this replaces the
 //     reference's separate _attn_bwd_preprocess launch). Per 32-key block:
 //       S^T = K Q^T, dP^T = V dO^T (K, V rows from LDS; Q, dO in registers),
-//       P = exp2(S*scale2 - LSE), dS = P (dP - Delta)   (lane-local LSE and Delta),
+//       P = exp2(S*scale2 - LSE) (one fp32 FMA per score, as the reference scales its fp32 scores:
+//       triton_sps_flash_attention.py:471), dS = P (dP - Delta)   (lane-local LSE and Delta),
 //       dQ^T += K^T dS^T  (K^T fragments via ds_read_b64_tr_b16).
 //  2. dK/dV pass (key-stationary). A workgroup owns 128 keys of one stream (natural, persistent
 //     or temporary), each wave 32 of them held in registers; it walks the 32-query chunks of the
 //     union of its lanes' query intervals (persistent keys: diagonal to document end; temporary
 //     keys: the w-token window):
 //       S = Q K^T, dP = dO V^T (Q, dO rows from LDS; K, V in registers),
+//       P = exp2(S*scale2 - LSE) (fp32 FMA per score, triton_sps_flash_attention.py:361),
 //       dV^T += dO^T P, dK^T += Q^T dS (dO^T, Q^T fragments via ds_read_b64_tr_b16).
 // Both passes consume their tiles in groups of four 32-row blocks (one barrier per group) through
 // the run_groups pipeline: buffer loads one group ahead into registers, double-buffered LDS; with
@@ -183,12 +185,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
     seed[m.N] = -delta;
   }
 
-  // Q pre-scaled by sm_scale * log2(e) (rounded to the input type) and the offsets folded into the
-  // MFMA accumulators: the S tile comes out as S * scale2 - lse and the dP tile as dP - Delta, so
-  // P = exp2(S') and dS = P * dP' cost one VALU operation per element each.
-#pragma unroll
-  for (int c = 0; c < D / 16; ++c) qf[c] = scale_frag<E>(qf[c], a.scale2);
-  const f32x16_t c_s = f32x16_t{} - lse, c_dp = f32x16_t{} - delta;
+  // The dP tile starts from -Delta, so it comes out of the MFMAs as dP - Delta and dS = P * dP' is one
+  // VALU operation per element; the S tile is scaled in fp32 (one FMA per score forms
+  // S * scale2 - LSE), never by rounding a scaled Q to the input type.
+  const float scale2 = a.scale2, neg_lse = -lse;
+  const f32x16_t c_dp = f32x16_t{} - delta;
 
   auto run = [&](auto exact_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
@@ -209,12 +210,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
         if ((act2 >> y) & 1) {
           const uint16_t* tK = sK[buf][y];
           const uint16_t* tV = sV[buf][y];
-          f32x16_t sc = c_s, dp = c_dp;
+          f32x16_t sc = f32x16_t{}, dp = c_dp;
 #pragma unroll
           for (int c = 0; c < D / 16; ++c) {
             sc = E::mfma(row_frag(tK, c), qf[c], sc);
             dp = E::mfma(row_frag(tV, c), dof[c], dp);
           }
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sc[e] = __builtin_fmaf(sc[e], scale2, neg_lse);
           if (!((full2 >> y) & 1))
             mask_partial<EXACT>(sc, lr, ws, t0, g,
                                 [&] { return qs_exact_bits(a, b, lr, plan.stream(i), t0, g, dq_doc); });
@@ -417,12 +420,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
     else
       issue_regs(0, 0);
     if (planned) k_lanes(m, run_end, st);
-    // K pre-scaled by sm_scale * log2(e) (rounded to the input type); the S and dP tiles start from
-    // the seeds -LSE and -Delta of their query rows, so they come out of the MFMAs as
-    // S * scale2 - LSE and dP - Delta: P = exp2(S') and dS = P * dP' cost one VALU operation per
-    // element each.
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) kf[c] = scale_frag<E>(kf[c], a.scale2);
+    // The dP tile starts from the -Delta seeds of its query rows, so it comes out of the MFMAs as
+    // dP - Delta and dS = P * dP' is one VALU operation per element; the S tile is scaled in fp32 by
+    // one FMA per score with the -LSE seeds (S * scale2 - LSE), never by rounding a scaled K.
+    const float scale2 = a.scale2;
     auto cls_of = [&](int i) { return classify_block(st.w, (st.c0 + i) * kBlock, EXACT); };
     const BlockMask bm = build_block_mask(nc, cls_of);
     auto body = [&](int j, int buf) {
@@ -435,7 +436,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
         if ((act2 >> y) & 1) {
           const uint16_t* tQ = sQ[buf][y];
           const uint16_t* tDO = sDO[buf][y];
-          f32x16_t sc, dp;
+          f32x16_t sc = f32x16_t{}, dp, nl;
 #pragma unroll
           for (int i4 = 0; i4 < 4; ++i4) {
             // Query rows 8*i4 + 4g + {0..3} of this chunk.
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
                 (const SPS_LDS float*)(&sSeed[buf][y][kBlock + 8 * i4 + 4 * g]));
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-              sc[4 * i4 + t] = l4[t];
+              nl[4 * i4 + t] = l4[t];
               dp[4 * i4 + t] = d4[t];
             }
           }
@@ -454,6 +455,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
             sc = E::mfma(row_frag(tQ, c), kf[c], sc);
             dp = E::mfma(row_frag(tDO, c), vf[c], dp);
           }
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sc[e] = __builtin_fmaf(sc[e], scale2, nl[e]);
           if (!((full2 >> y) & 1))
             mask_partial<EXACT>(sc, st.r, st.w, qc, g,
                                 [&] { return ks_exact_bits(a, b, kp, st.r.hi, qc, g, dk_doc); });

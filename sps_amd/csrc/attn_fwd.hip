@@ -16,12 +16,14 @@
 // swizzled tiles (run_groups_dma), below through registers into padded tiles (run_pairs). Rows past
 // the end of the sequence read as zeros.
 //
-// Softmax: exp2 domain. Q is pre-scaled by sm_scale * log2(e) (rounded to the input type, as the
-// backward passes do) and the score MFMAs start from -m_run, so they deliver S * scale2 - m_run and
-// P = exp2 of the accumulator costs one VALU operation per element (the forward is VALU-bound at
-// D = 64: this took it from 70 to 67 us at the benchmark shape). The running max is only raised (and
-// the accumulator rescaled) when a block's max exceeds it by more than 2^8, so P stays <= 256 and
-// most blocks skip the rescale; row sums of P use v_dot2 on the packed 16-bit P the MFMA consumes.
+// Softmax: exp2 domain. The score MFMAs deliver S = K Q^T in fp32 from the unscaled inputs, and one
+// FMA per score forms S * sm_scale * log2(e) - m_run in fp32, as the reference scales its fp32 scores
+// (triton_sps_flash_attention.py:78-79): scaling an input operand instead would round Q * scale to
+// the input type, an error that grows with the score magnitude. Masks are applied to the scaled
+// scores, so any scale (zero or negative too) keeps masked keys at -inf. The running max is only
+// raised (and the accumulator rescaled) when a block's max exceeds it by more than 2^8, so P stays
+// <= 256 and most blocks skip the rescale; row sums of P use v_dot2 on the packed 16-bit P the MFMA
+// consumes.
 //
 // Reference semantics: _attn_fwd_sps / _attn_fwd_inner_sps (triton_sps_flash_attention.py:26-269),
 // _attn_fwd (triton_reverse_sps_flash_attention.py:242-331, triton_full_flash_attention.py:204-283):
@@ -164,9 +166,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
     if (nb > 0) issue_dma(0, 0);
 
   if (planned) q_lanes(m, qp, run_start, st);
-#pragma unroll
-  for (int c = 0; c < D / 16; ++c) qf[c] = scale_frag<E>(qf[c], a.scale2);
-  f32x16_t cm = f32x16_t{};  // -m_run (0 while no score seen): the score MFMAs start from it
+  const float scale2 = a.scale2;
+  float negm = 0.f;  // -m_run (0 while no score has been seen): the per-score FMA subtracts m_run
 
   // The pair's max (relative to m_run) must exceed thr to raise m_run: any score while none has been
   // seen, then the lazy-rescale threshold.
@@ -194,9 +195,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
 #pragma unroll
       for (int y = 0; y < 2; ++y) {
         const uint16_t* kt = tK(buf, y);
-        sc[y] = E::mfma(row_frag(kt, 0), qf[0], cm);
+        sc[y] = E::mfma(row_frag(kt, 0), qf[0], f32x16_t{});
 #pragma unroll
         for (int c = 1; c < D / 16; ++c) sc[y] = E::mfma(row_frag(kt, c), qf[c], sc[y]);
+      }
+      // Scaled scores relative to the running max: S * scale2 - m_run, in fp32.
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[y][e] = __builtin_fmaf(sc[y][e], scale2, negm);
       }
       if (full2 != 3) {
 #pragma unroll
@@ -213,7 +220,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
           }
         }
       }
-      // Scores come out as S * scale2 - m_run: the pair's max relative to the running max.
+      // The pair's max relative to the running max.
       const float mb = half_max(max32(sc[0], sc[1]));
       const bool need = mb > thr;
       if (wave_any(need)) {
@@ -228,7 +235,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
         for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
 #pragma unroll
         for (int y = 0; y < 2; ++y) sc[y] -= sh;
-        cm = f32x16_t{} - (m_run == -INFINITY ? 0.f : m_run);
+        negm = m_run == -INFINITY ? 0.f : -m_run;
       }
 #pragma unroll
       for (int y = 0; y < 2; ++y) {

@@ -135,16 +135,6 @@ struct DmaTile {
   }
 };
 
-// An 8-element fragment multiplied by `s`, rounded back to the element type.
-template <class E>
-__device__ __forceinline__ u32x4_t scale_frag(u32x4_t f, float s) {
-  u32x4_t r;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    r[j] = E::pack2(E::to_f32((uint16_t)(f[j] & 0xffffu)) * s, E::to_f32((uint16_t)(f[j] >> 16)) * s);
-  return r;
-}
-
 // Descriptor over the rows [0, N) of one (batch, head) slice of a [B, H, N, D] tensor.
 template <int D>
 __device__ __forceinline__ BufRsrc head_rsrc(const uint16_t* head_base, int64_t sn, int N) {

@@ -129,13 +129,15 @@ int setup_common(sps::AttnArgs& a, int family, int B, int H, int N, const void* 
   return SPS_OK;
 }
 
-int check_scale(float sm_scale) {
-  if (!(sm_scale > 0.f) || !std::isfinite(sm_scale))
-    return fail(SPS_E_UNSUPPORTED, "sm_scale must be finite and > 0 (got %g)", (double)sm_scale);
-  return SPS_OK;
+}  // namespace
+
+// Error reporting for the entry points defined in other translation units (hidden: not part of the
+// library's exported interface).
+extern "C" __attribute__((visibility("hidden"))) int sps_capi_fail(int code, const char* msg) {
+  return fail(code, "%s", msg);
 }
 
-}  // namespace
+extern "C" __attribute__((visibility("hidden"))) void sps_capi_clear() { g_last_error.clear(); }
 
 extern "C" {
 
@@ -167,7 +169,6 @@ int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype, const void* 
   if (!supported_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "head_dim %d not supported", D);
   if (dtype != SPS_DTYPE_BF16 && dtype != SPS_DTYPE_F16)
     return fail(SPS_E_UNSUPPORTED, "attention dtype code %d not supported (bf16, f16)", dtype);
-  if ((rc = check_scale(sm_scale))) return rc;
   const int need = (int64_t)B * H * N > 0;
   if ((rc = check_tensor("q", q, q_strides, need, N, D)) || (rc = check_tensor("k", k, k_strides, need, N, D)) ||
       (rc = check_tensor("v", v, v_strides, need, N, D)) || (rc = check_tensor("o", o, o_strides, need, N, D)))
@@ -209,7 +210,6 @@ static int attn_bwd_impl(int passes, int family, int B, int H, int N, int D, int
   if (!supported_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "head_dim %d not supported", D);
   if (dtype != SPS_DTYPE_BF16 && dtype != SPS_DTYPE_F16)
     return fail(SPS_E_UNSUPPORTED, "attention dtype code %d not supported (bf16, f16)", dtype);
-  if ((rc = check_scale(sm_scale))) return rc;
   const int need = (int64_t)B * H * N > 0;
   if ((rc = check_tensor("q", q, q_strides, need, N, D)) || (rc = check_tensor("k", k, k_strides, need, N, D)) ||
       (rc = check_tensor("v", v, v_strides, need, N, D)) || (rc = check_tensor("o", o, o_strides, need, N, D)) ||

@@ -8,6 +8,12 @@ model.py:160-199). ``rope_qkv_for_attention(q, k, v, freqs_cis)`` is the whole p
 the attention modules (sps/core.py:45-55, reverse_sps/core.py:60-75): RoPE on Q and K, every tensor
 cast to bf16 and handed over as the [B, H, N, D] transposed views of [B, N, H, D] buffers, in one
 launch. Both run in libsps_attn.so (``sps_rope_qkv``); there is no CPU path.
+
+Both are differentiable. The rotation by a unit complex frequency f is a real-linear map whose
+adjoint is the rotation by conj(f), and the casts pass gradients through in the input's dtype (the
+autograd of model.py:201-230's ``.float()`` / ``view_as_complex`` / ``* freqs_cis`` / ``type_as``), so
+the backward is the same kernel on the incoming gradients with the conjugate frequencies (V's
+gradient is cast back to V's dtype in the same launch).
 """
 
 from __future__ import annotations
@@ -63,13 +69,55 @@ def _launch(q: Tensor, k: Tensor, v: Optional[Tensor], freqs_cis: Tensor, q_out:
     N.check("sps_rope_qkv", status)
 
 
+class _RopePair(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, xq, xk, freqs_cis):
+        q_out = torch.empty(xq.shape, device=xq.device, dtype=xq.dtype)
+        k_out = torch.empty(xk.shape, device=xk.device, dtype=xk.dtype)
+        _launch(xq, xk, None, freqs_cis, q_out, k_out, None)
+        ctx.save_for_backward(freqs_cis)
+        return q_out, k_out
+
+    @staticmethod
+    def backward(ctx, gq, gk):
+        (freqs_cis,) = ctx.saved_tensors
+        ref = gq if gq is not None else gk
+        gq = gq if gq is not None else torch.zeros_like(ref)
+        gk = gk if gk is not None else torch.zeros_like(ref)
+        dq = torch.empty(gq.shape, device=gq.device, dtype=gq.dtype)
+        dk = torch.empty(gk.shape, device=gk.device, dtype=gk.dtype)
+        _launch(gq, gk.to(gq.dtype), None, _conj(freqs_cis), dq, dk, None)
+        return dq, dk, None
+
+
+class _RopeQKV(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, freqs_cis, out_dtype):
+        outs = [torch.empty(q.shape, device=q.device, dtype=out_dtype) for _ in range(3)]
+        _launch(q, k, v, freqs_cis, *outs)
+        ctx.save_for_backward(freqs_cis)
+        ctx.in_dtype = q.dtype
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, gq, gk, gv):
+        (freqs_cis,) = ctx.saved_tensors
+        ref = next(g for g in (gq, gk, gv) if g is not None)
+        gq, gk, gv = (g if g is not None else torch.zeros_like(ref) for g in (gq, gk, gv))
+        dt = gq.dtype
+        outs = [torch.empty(gq.shape, device=gq.device, dtype=ctx.in_dtype) for _ in range(3)]
+        _launch(gq, gk.to(dt), gv.to(dt), _conj(freqs_cis), *outs)
+        return outs[0], outs[1], outs[2], None, None
+
+
+def _conj(freqs_cis: Tensor) -> Tensor:
+    return freqs_cis.conj().resolve_conj()
+
+
 def apply_rotary_emb(xq: Tensor, xk: Tensor, freqs_cis: Tensor) -> Tuple[Tensor, Tensor]:
     """RoPE on [B, T, H, D] queries and keys; returns new tensors of the inputs' dtype and shape."""
     assert xq.ndim == 4 and xk.shape == xq.shape
-    q_out = torch.empty(xq.shape, device=xq.device, dtype=xq.dtype)
-    k_out = torch.empty(xk.shape, device=xk.device, dtype=xk.dtype)
-    _launch(xq, xk, None, freqs_cis, q_out, k_out, None)
-    return q_out, k_out
+    return _RopePair.apply(xq, xk, freqs_cis)
 
 
 def rope_qkv_for_attention(q: Tensor, k: Tensor, v: Tensor, freqs_cis: Tensor,
@@ -80,6 +128,5 @@ def rope_qkv_for_attention(q: Tensor, k: Tensor, v: Tensor, freqs_cis: Tensor,
     full_attention."""
     assert q.ndim == 4 and k.shape == q.shape and v.shape == q.shape
     assert out_dtype in _FLOAT_DTYPES
-    outs = [torch.empty(q.shape, device=q.device, dtype=out_dtype) for _ in range(3)]
-    _launch(q, k, v, freqs_cis, *outs)
+    outs = _RopeQKV.apply(q, k, v, freqs_cis, out_dtype)
     return tuple(t.transpose(1, 2) for t in outs)

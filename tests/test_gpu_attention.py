@@ -318,3 +318,58 @@ def test_backward_reusing_forward_layout_is_identical(family):
                                   between_passes=lambda: None)
     for r, x, y in zip(ref, got, split):
         assert torch.equal(r, x) and torch.equal(r, y)
+
+
+# Activation scales seen in trained models: Q and K drawn with standard deviation 4 and 8, so the
+# scaled scores reach tens of units and the softmax is sharp. The kernels scale the fp32 scores
+# (S * sm_scale * log2 e, as triton_sps_flash_attention.py:78-79 does), so the forward keeps the
+# standard bound. The gradients go through bf16/f16-rounded P and dS, as the reference's own
+# kernels do (triton_sps_flash_attention.py:361-377); dQ and dK grow with the Q/K scale s and with
+# sm_scale, so their absolute bound is 2e-2 * s * max(1, |sm_scale| * sqrt(D)). With these inputs, an exact emulation of the reference's algorithm
+# (fp32 scores, 16-bit P and dS) measures up to 1.6x that bound on bf16 dK at s = 4 and 0.7x at
+# s = 8; the test allows 2.5x. Rounding a pre-scaled Q to bf16 instead (an earlier formulation of
+# these kernels) measures 5x in the forward and 17x on the gradients at s = 8.
+GRAD_FACTOR = 2.5
+
+
+def _scaled_check(family, n, d, s, dtype, window=64, sm_scale=None, seed=0):
+    dev = torch.device("cuda")
+    b, h = 1, 2
+    g = torch.Generator().manual_seed(seed)
+    q, k = ((torch.randn((b, h, n, d), generator=g) * s).to(dtype) for _ in range(2))
+    v, do = (torch.randn((b, h, n, d), generator=g).to(dtype) for _ in range(2))
+    rng = np.random.default_rng(seed)
+    tokens = n if family == "full" else n // 2
+    docs = _packed_docs(rng, b, tokens, family, max_len=tokens)
+    scale = 1.0 / math.sqrt(d) if sm_scale is None else sm_scale
+    qg, kg, vg = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+    out = API[family](qg, kg, vg, scale, window, torch.tensor(docs, device=dev), None)
+    out.backward(do.to(dev))
+    mask = M.batch_mask(FAMILY[family], docs, n=n, window=window, batch=b)
+    qn, kn, vn, don = (t.float().numpy() for t in (q, k, v, do))
+    o_ref, _ = A.forward(qn, kn, vn, mask, scale)
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(o_ref).float(), atol=ATOL, rtol=RTOL)
+    dq, dk, dv = A.backward(qn, kn, vn, don, mask, scale)
+    for name, got, want, grows in (("dq", qg.grad, dq, True), ("dk", kg.grad, dk, True), ("dv", vg.grad, dv, False)):
+        want = torch.from_numpy(want)
+        err = (got.double().cpu() - want).abs()
+        grad_scale = s * max(1.0, abs(scale) * math.sqrt(d)) if grows else 1.0
+        bound = ATOL * grad_scale + RTOL * want.abs()
+        ratio = float((err / bound).max())
+        assert ratio <= GRAD_FACTOR, f"{name}: max error / bound = {ratio:.2f} (max abs error {float(err.max()):.4g})"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("s", [4.0, 8.0])
+@pytest.mark.parametrize("family", ["sps", "full"])
+def test_scaled_activations(family, s, dtype):
+    _scaled_check(family, 512, 64, s, dtype)
+
+
+@pytest.mark.parametrize("sm_scale", [-0.125, 0.0, 1.0])
+@pytest.mark.parametrize("family", ["sps", "reverse_sps", "full"])
+def test_any_sm_scale(family, sm_scale):
+    # The reference takes any sm_scale (it multiplies the fp32 scores by it); masks are applied to the
+    # scaled scores, so a zero scale gives the mean of the visible values and a negative one flips
+    # the scores.
+    _scaled_check(family, 256, 64, 1.0, torch.bfloat16, window=5, sm_scale=sm_scale, seed=3)

@@ -163,3 +163,36 @@ def test_q2_error_conventions():
         DA.triton_segmented_q2_attention(q, [seg], current_normal_k_BxHxD=cur, current_normal_v_BxHxD=cur,
                                          current_predict_k_BxHxD=cur, current_predict_v_BxHxD=cur,
                                          attn_dtype=torch.bfloat16)
+
+
+def test_installed_shim_sends_cuda_calls_to_the_kernel(monkeypatch):
+    # After install_into_modeling, the reference module's masked_kv_attention name reaches the HIP
+    # kernel for CUDA tensors (bit-identical to calling sps_amd directly) and the module's original
+    # function for CPU tensors (reference: decode_attention.py:597-704).
+    import sys
+    import types
+
+    import sps_amd
+
+    mod = types.ModuleType("modeling.models.utils.decode_attention")
+    seen = []
+
+    def original(q_BxHxD, segments, **kwargs):
+        seen.append(q_BxHxD.device.type)
+        return torch.zeros(q_BxHxD.shape, dtype=torch.float32)
+
+    mod.masked_kv_attention = original
+    monkeypatch.setitem(sys.modules, mod.__name__, mod)
+    sps_amd.install_into_modeling()
+    g = torch.Generator().manual_seed(4)
+    b, h, d, storage = 3, 2, 64, 50
+    k, v = (torch.randn((b, h, storage, d), generator=g).to(torch.bfloat16).cuda() for _ in range(2))
+    lens = torch.tensor([5, 50, 17], device="cuda")
+    q = torch.randn((b, h, d), generator=g).to(torch.bfloat16).cuda()
+    seg = [DA.KVSegment(k, v, lens)]
+    got = mod.masked_kv_attention(q, seg, attn_dtype=torch.bfloat16)
+    want = DA.masked_kv_attention(q, seg, attn_dtype=torch.bfloat16)
+    assert got.is_cuda and torch.equal(got, want)
+    assert seen == []
+    mod.masked_kv_attention(q.cpu(), [DA.KVSegment(k.cpu(), v.cpu(), lens.cpu())], attn_dtype=torch.float32)
+    assert seen == ["cpu"]

@@ -89,3 +89,65 @@ def test_fused_pre_attention_feeds_the_attention_kernel():
     vr = v.transpose(1, 2).to(torch.bfloat16)
     y_ref = sps_sliding_attention(qr, kr, vr, 1 / math.sqrt(D), 16, documents_idx_BxT=docs)
     torch.testing.assert_close(y.float(), y_ref.float(), atol=2e-2, rtol=1e-2)
+
+
+def _reference_rope_autograd(x64, f):
+    # The reference's op sequence (model.py:201-230: view_as_complex of the fp32 input, times the
+    # complex frequencies, view_as_real), in float64 on the CPU, differentiated by torch autograd.
+    z = torch.view_as_complex(x64.reshape(*x64.shape[:-1], -1, 2))
+    ff = f.to(torch.complex128)
+    ff = ff.view(1, ff.shape[0], 1, ff.shape[1]) if ff.ndim == 2 else ff.view(ff.shape[0], ff.shape[1], 1, ff.shape[2])
+    return torch.view_as_real(z * ff).flatten(3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("per_sequence", [False, True])
+def test_apply_rotary_emb_gradients(dtype, per_sequence):
+    # The rotation is linear, so the gradient of sum(out * g) is the inverse rotation of g: the
+    # backward runs the kernel with the conjugate frequencies. Checked against autograd of the
+    # reference formula (one rounding of the result to `dtype`).
+    g = torch.Generator().manual_seed(11)
+    B, T, H, D = 2, 17, 3, 32
+    xq, xk, gq, gk = (torch.randn(B, T, H, D, generator=g).to(dtype) for _ in range(4))
+    table = _freqs(D, 32)
+    f = table[torch.randint(0, 32, (B, T), generator=g)] if per_sequence else table[:T]
+    q = xq.cuda().requires_grad_(True)
+    k = xk.cuda().requires_grad_(True)
+    qo, ko = SR.apply_rotary_emb(q, k, f.cuda())
+    (qo.float() * gq.cuda().float()).sum().add((ko.float() * gk.cuda().float()).sum()).backward()
+    for x, grad_out, got in ((xq, gq, q.grad), (xk, gk, k.grad)):
+        x64 = x.double().requires_grad_(True)
+        (_reference_rope_autograd(x64, f) * grad_out.double()).sum().backward()
+        assert got.dtype == dtype
+        _check(got, x64.grad.numpy(), dtype)
+
+
+def test_rope_qkv_for_attention_gradients_reach_the_projection():
+    # Training path: projection (fp32, requires grad) -> fused RoPE + bf16 casts -> attention. The
+    # gradient reaching the projection equals the one through the reference's op sequence, with the
+    # same attention backward feeding both.
+    g = torch.Generator().manual_seed(5)
+    B, T, H, D = 1, 64, 2, 64
+    qkv = torch.randn(B, 2 * T, 3 * H * D, generator=g)
+    f = _freqs(D, 2 * T)
+    do = torch.randn(B, H, 2 * T, D, generator=g).to(torch.bfloat16).cuda()
+
+    def run(fused):
+        x = qkv.cuda().requires_grad_(True)
+        q, k, v = (t.view(B, 2 * T, H, D) for t in x.split(H * D, dim=2))
+        if fused:
+            qa, ka, va = SR.rope_qkv_for_attention(q, k, v, f.cuda())
+        else:
+            zq = torch.view_as_complex(q.float().reshape(B, 2 * T, H, -1, 2))
+            zk = torch.view_as_complex(k.float().reshape(B, 2 * T, H, -1, 2))
+            ff = f.cuda().view(1, 2 * T, 1, D // 2)
+            qa = torch.view_as_real(zq * ff).flatten(3).transpose(1, 2).to(torch.bfloat16)
+            ka = torch.view_as_real(zk * ff).flatten(3).transpose(1, 2).to(torch.bfloat16)
+            va = v.transpose(1, 2).to(torch.bfloat16)
+        out = sps_sliding_attention(qa, ka, va, 1 / math.sqrt(D), 8)
+        out.backward(do)
+        return x.grad
+
+    got, want = run(True), run(False)
+    assert got is not None and torch.isfinite(got).all()
+    torch.testing.assert_close(got, want, atol=2e-2, rtol=1e-2)

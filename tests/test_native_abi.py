@@ -1,5 +1,6 @@
 """The C-ABI library loads, exports what include/sps_attn.h declares, and validates arguments
-before touching the GPU (CPU-only: every call here fails validation, so no kernel is launched)."""
+before touching the GPU. The validation calls pass fake device addresses, so they run only where no
+GPU is visible: a call whose arguments passed validation could otherwise launch a kernel on them."""
 
 import ctypes as C
 import re
@@ -29,6 +30,15 @@ def test_library_exports_every_declared_symbol():
     assert lib.sps_version().startswith(b"sps_attn")
 
 
+def _no_gpu() -> bool:
+    import torch
+
+    return not torch.cuda.is_available()
+
+
+cpu_only = pytest.mark.skipif(not _no_gpu(), reason="fake device addresses: CPU build only")
+
+
 def _fwd(**over):
     args = dict(family=1, B=1, H=1, N=64, D=64, dtype=N.DTYPE_BF16, sm_scale=0.125, window=4, has_pkw=0, pkw=-1,
                 docs=None, docs_dtype=N.DTYPE_I64, ws=None, ws_bytes=0, ptr=0x10000, strides=(64 * 64, 64 * 64, 64))
@@ -48,22 +58,22 @@ def _fwd(**over):
     [
         (dict(family=7), N.SPS_E_INVALID, "family"),
         (dict(N=63), N.SPS_E_INVALID, "even"),
-        (dict(D=256), N.SPS_E_UNSUPPORTED, "head_dim"),
+        (dict(D=512), N.SPS_E_UNSUPPORTED, "head_dim"),
         (dict(D=48), N.SPS_E_UNSUPPORTED, "head_dim"),
         (dict(dtype=N.DTYPE_F32), N.SPS_E_UNSUPPORTED, "dtype"),
-        (dict(sm_scale=0.0), N.SPS_E_UNSUPPORTED, "sm_scale"),
-        (dict(sm_scale=float("nan")), N.SPS_E_UNSUPPORTED, "sm_scale"),
         (dict(ptr=0x10008), N.SPS_E_INVALID, "aligned"),
         (dict(strides=(64 * 64, 64 * 64, 60)), N.SPS_E_INVALID, "multiple of 8"),
         (dict(docs=0x30000, docs_dtype=N.DTYPE_F32), N.SPS_E_INVALID, "int32 or int64"),
         (dict(docs=0x30000, docs_dtype=N.DTYPE_I64, ws_bytes=0), N.SPS_E_WORKSPACE, "workspace"),
     ],
 )
+@cpu_only
 def test_forward_argument_validation(over, code, needle):
     assert _fwd(**over) == code
     assert needle in N.last_error()
 
 
+@cpu_only
 def test_empty_problem_is_a_noop():
     assert _fwd(B=0) == N.SPS_OK
     assert _fwd(N=0) == N.SPS_OK
@@ -88,6 +98,7 @@ def _decode(nq=1, D=64, n_seg=0, q_dtype=N.DTYPE_BF16, extra_dtype=N.DTYPE_BF16,
                               None, z, n_extra, None, None, extra_dtype, z, None, 0.125, 0x2000, z, None, 0, None)
 
 
+@cpu_only
 def test_decode_argument_validation():
     assert _decode(nq=3) == N.SPS_E_INVALID and "nq" in N.last_error()
     assert _decode(D=48) == N.SPS_E_UNSUPPORTED
@@ -103,6 +114,7 @@ def test_last_error_truncates():
     assert full > 7 and len(buf.value) == 7
 
 
+@cpu_only
 def test_backward_pass_selector_validation():
     lib = N.lib()
     st = N.i64_array((64 * 64, 64 * 64, 64))
@@ -122,6 +134,7 @@ def _kv_update(window=2, ring_storage=4, kv_dtype=N.DTYPE_BF16, new_dtype=N.DTYP
                                  len_dtype, new_dtype, p, p, p, p, z, p, active_dtype, 1, None)
 
 
+@cpu_only
 def test_kv_update_argument_validation():
     assert _kv_update(window=5, ring_storage=4) == N.SPS_E_INVALID and "ring storage" in N.last_error()
     assert _kv_update(kv_dtype=N.DTYPE_I32) == N.SPS_E_UNSUPPORTED and "cache dtype" in N.last_error()
@@ -139,6 +152,7 @@ def _rope(D=64, in_dtype=N.DTYPE_F32, ptr=0x10000, st=(4096, 64, 64)):
                                 0x30000, s, 0x30000, s, None, None, None)
 
 
+@cpu_only
 def test_rope_argument_validation():
     assert _rope(D=12) == N.SPS_E_UNSUPPORTED and "multiple of 8" in N.last_error()
     assert _rope(in_dtype=N.DTYPE_I32) == N.SPS_E_UNSUPPORTED and "input dtype" in N.last_error()

@@ -51,3 +51,19 @@ def test_padded_masked_kv_attention_matches_oracle():
                      [(ex[0][0].numpy(), ex[0][1].numpy())], [1], 1)[:, 0]
     np.testing.assert_allclose(got.numpy(), want, atol=1e-5)
     assert math.isfinite(float(got.abs().max()))
+
+
+import pytest
+
+
+@pytest.mark.parametrize("family,window", [(1, 3), (1, 0), (2, 4), (1, 64)])
+def test_stepwise_decode_path_matches_dense_oracle(family, window):
+    # The token-by-token CPU path (ring + retained + current keys per slot) computes the same
+    # attention as the dense masked forward over the interleaved sequence of one document.
+    g = torch.Generator().manual_seed(family * 10 + window)
+    b, h, t, d = 2, 2, 20, 16
+    q, k, v = (torch.randn((b, h, 2 * t, d), generator=g) for _ in range(3))
+    got = CF.stepwise_sps_forward(q, k, v, family, window)
+    mask = M.batch_mask(family, None, n=2 * t, window=window, batch=b)
+    want, _ = A.forward(q.numpy(), k.numpy(), v.numpy(), mask, 1 / math.sqrt(d))
+    np.testing.assert_allclose(got.numpy(), want, atol=1e-5)
