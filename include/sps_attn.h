@@ -189,6 +189,28 @@ int sps_decode(int B, int H, int D, int nq,
                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * sps_decode without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The per-chunk partial records go to a scratch array of 16 MiB that the library holds
+ * on each GPU it runs on (a file-scope device array, resolved per device on that device's first
+ * call); the call allocates nothing. Returns SPS_E_UNSUPPORTED when the records would need more than
+ * 16 MiB (sps_decode_workspace_bytes for the same arguments). Every call on one GPU shares that
+ * GPU's array, so calls that overlap on one GPU (different streams, no ordering between them) race;
+ * calls ordered on one stream are safe. The array keeps the last call's records, and no call reads
+ * records it did not write. Arguments otherwise as sps_decode.
+ */
+int sps_decode_static(int B, int H, int D, int nq,
+                      const void* q, int q_dtype, const int64_t* q_strides,
+                      int kv_dtype, int n_seg,
+                      const void* const* seg_k, const int64_t* seg_k_strides,
+                      const void* const* seg_v, const int64_t* seg_v_strides,
+                      const void* const* seg_len, const int* seg_len_dtype, const int* seg_len_per_head,
+                      const int64_t* seg_scan,
+                      int n_extra, const void* const* extra_k, const void* const* extra_v, int extra_dtype,
+                      const int64_t* extra_strides, const int* extra_query_mask,
+                      float sm_scale, float* out, const int64_t* out_strides, void* stream);
+
+/*
  * Decode KV-cache update of one layer, one launch (replaces fused_sps_kv_update,
  * utils/decode_attention_fast.py:139-221; semantics of the un-fused path it replaces,
  * _update_normal_memory_unfused / _update_predict_memory_unfused, reverse_sps/inference.py:137-168

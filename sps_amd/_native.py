@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "sps_attn_mask",
     "sps_decode_workspace_bytes",
     "sps_decode",
+    "sps_decode_static",
     "sps_kv_update",
     "sps_rope_qkv",
     "sps_prefill_to_decode",
@@ -100,6 +101,13 @@ _SIGNATURES = {
         + [C.POINTER(_p), _pi64, C.POINTER(_p), _pi64, C.POINTER(_p), _pi32, _pi32, _pi64]
         + [_i32, C.POINTER(_p), C.POINTER(_p), _i32, _pi64, _pi32]
         + [_f32, _p, _pi64, _p, _sz, _p],
+    ),
+    "sps_decode_static": (
+        _i32,
+        [_i32, _i32, _i32, _i32, _p, _i32, _pi64, _i32, _i32]
+        + [C.POINTER(_p), _pi64, C.POINTER(_p), _pi64, C.POINTER(_p), _pi32, _pi32, _pi64]
+        + [_i32, C.POINTER(_p), C.POINTER(_p), _i32, _pi64, _pi32]
+        + [_f32, _p, _pi64, _p],
     ),
     "sps_kv_update": (
         _i32,

@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/sps_attn.h"
@@ -305,14 +306,17 @@ size_t sps_decode_workspace_bytes(int B, int H, int D, int nq, int kv_dtype, int
   return align_up(bytes);
 }
 
-int sps_decode(int B, int H, int D, int nq, const void* q, int q_dtype, const int64_t* q_strides, int kv_dtype,
-               int n_seg, const void* const* seg_k, const int64_t* seg_k_strides, const void* const* seg_v,
-               const int64_t* seg_v_strides, const void* const* seg_len, const int* seg_len_dtype,
-               const int* seg_len_per_head, const int64_t* seg_scan, int n_extra, const void* const* extra_k,
-               const void* const* extra_v, int extra_dtype, const int64_t* extra_strides,
-               const int* extra_query_mask, float sm_scale, float* out, const int64_t* out_strides,
-               void* workspace, size_t workspace_bytes, void* stream) {
-  g_last_error.clear();
+}  // extern "C"
+
+// Validation and launch shared by sps_decode (caller's workspace) and sps_decode_static (the
+// library's scratch array). `workspace` is only read after `workspace_bytes` has been checked.
+static int decode_impl(int B, int H, int D, int nq, const void* q, int q_dtype, const int64_t* q_strides,
+                       int kv_dtype, int n_seg, const void* const* seg_k, const int64_t* seg_k_strides,
+                       const void* const* seg_v, const int64_t* seg_v_strides, const void* const* seg_len,
+                       const int* seg_len_dtype, const int* seg_len_per_head, const int64_t* seg_scan, int n_extra,
+                       const void* const* extra_k, const void* const* extra_v, int extra_dtype,
+                       const int64_t* extra_strides, const int* extra_query_mask, float sm_scale, float* out,
+                       const int64_t* out_strides, void* workspace, size_t workspace_bytes, void* stream) {
   if (B < 0 || H < 0) return fail(SPS_E_INVALID, "negative size B=%d H=%d", B, H);
   if (nq != 1 && nq != 2) return fail(SPS_E_INVALID, "nq must be 1 or 2 (got %d)", nq);
   if (!decode_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "decode head_dim %d not supported", D);
@@ -403,6 +407,81 @@ int sps_decode(int B, int H, int D, int nq, const void* q, int q_dtype, const in
   a.scale2 = sm_scale * 1.4426950408889634f;
   a.part = static_cast<float*>(workspace);
   return hip_status(sps::launch_decode(a, D, kv_dtype, static_cast<hipStream_t>(stream)), "decode");
+}
+
+// Scratch of sps_decode_static: the per-chunk partial records live in this array instead of a
+// caller-provided workspace. Each GPU holds its own copy, at its own address, for the life of the
+// process. In host code `decode_scratch` names a host-side stand-in, not device memory: its device
+// address comes from hipGetSymbolAddress, once per device, on that device's first call.
+constexpr size_t kDecodeScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char decode_scratch[kDecodeScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of the current device's copy of decode_scratch.
+int decode_scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(SPS_E_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(SPS_E_UNSUPPORTED, "device %d: the scratch table covers devices 0..%d", dev, kMaxScratchDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(decode_scratch));
+    if (e != hipSuccess || !p)
+      return fail(SPS_E_HIP, "hipGetSymbolAddress(decode_scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SPS_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int sps_decode(int B, int H, int D, int nq, const void* q, int q_dtype, const int64_t* q_strides, int kv_dtype,
+               int n_seg, const void* const* seg_k, const int64_t* seg_k_strides, const void* const* seg_v,
+               const int64_t* seg_v_strides, const void* const* seg_len, const int* seg_len_dtype,
+               const int* seg_len_per_head, const int64_t* seg_scan, int n_extra, const void* const* extra_k,
+               const void* const* extra_v, int extra_dtype, const int64_t* extra_strides,
+               const int* extra_query_mask, float sm_scale, float* out, const int64_t* out_strides,
+               void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  return decode_impl(B, H, D, nq, q, q_dtype, q_strides, kv_dtype, n_seg, seg_k, seg_k_strides, seg_v,
+                     seg_v_strides, seg_len, seg_len_dtype, seg_len_per_head, seg_scan, n_extra, extra_k, extra_v,
+                     extra_dtype, extra_strides, extra_query_mask, sm_scale, out, out_strides, workspace,
+                     workspace_bytes, stream);
+}
+
+int sps_decode_static(int B, int H, int D, int nq, const void* q, int q_dtype, const int64_t* q_strides,
+                      int kv_dtype, int n_seg, const void* const* seg_k, const int64_t* seg_k_strides,
+                      const void* const* seg_v, const int64_t* seg_v_strides, const void* const* seg_len,
+                      const int* seg_len_dtype, const int* seg_len_per_head, const int64_t* seg_scan, int n_extra,
+                      const void* const* extra_k, const void* const* extra_v, int extra_dtype,
+                      const int64_t* extra_strides, const int* extra_query_mask, float sm_scale, float* out,
+                      const int64_t* out_strides, void* stream) {
+  g_last_error.clear();
+  if (n_seg < 0 || n_seg > sps::kMaxDecodeSegs)
+    return fail(SPS_E_INVALID, "at most %d segments (got %d)", sps::kMaxDecodeSegs, n_seg);
+  if (n_seg > 0 && !seg_scan) return fail(SPS_E_INVALID, "seg_scan: null pointer");
+  const size_t need = sps_decode_workspace_bytes(B, H, D, nq, kv_dtype, n_seg, seg_scan);
+  if (need > kDecodeScratchBytes)
+    return fail(SPS_E_UNSUPPORTED,
+                "sps_decode_static: the partial records need %zu bytes, more than the %zu-byte scratch "
+                "array (use sps_decode with a workspace)", need, kDecodeScratchBytes);
+  void* ptr = nullptr;
+  if ((int64_t)B * H > 0) {
+    const int rc = decode_scratch_ptr(&ptr);
+    if (rc) return rc;
+  }
+  return decode_impl(B, H, D, nq, q, q_dtype, q_strides, kv_dtype, n_seg, seg_k, seg_k_strides, seg_v,
+                     seg_v_strides, seg_len, seg_len_dtype, seg_len_per_head, seg_scan, n_extra, extra_k, extra_v,
+                     extra_dtype, extra_strides, extra_query_mask, sm_scale, out, out_strides, ptr,
+                     kDecodeScratchBytes, stream);
 }
 
 int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v, const int64_t* ring_strides,

@@ -69,9 +69,10 @@ def _as_attn(t: Tensor, attn_dtype: torch.dtype) -> Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
-def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor) -> Tensor:
+def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor, static_scratch: bool = False) -> Tensor:
     """Calls sps_decode. q: [B, nq, H, D] (bf16/f16/f32); extras: list of (k, v) [B, H, D] sharing one
-    dtype and one (b, h) stride pair."""
+    dtype and one (b, h) stride pair. ``static_scratch`` calls sps_decode_static instead, which keeps
+    its partial records in the library's own scratch array (no workspace is allocated)."""
     b, _, h, d = q.shape
     kv_dtype = N.DTYPE_BF16
     if segments:
@@ -80,8 +81,10 @@ def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor) 
     lens = [s.lengths.contiguous() for s in segments]
     lib = N.lib()
     scan_arr = N.i64_array(scans)
-    ws_bytes = lib.sps_decode_workspace_bytes(b, h, d, nq, kv_dtype, len(segments), scan_arr)
-    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
+    ws = None
+    if not static_scratch:
+        ws_bytes = lib.sps_decode_workspace_bytes(b, h, d, nq, kv_dtype, len(segments), scan_arr)
+        ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
     k_strides, v_strides = [], []
     for s in segments:
         k_strides += [s.k.stride(0), s.k.stride(1), s.k.stride(2)]
@@ -90,7 +93,9 @@ def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor) 
     ev = [e[1] for e in extras]
     e_strides = (ek[0].stride(0), ek[0].stride(1)) if extras else (0, 0)
     e_dtype = _KV_DTYPES[ek[0].dtype] if extras else N.DTYPE_F32
-    status = lib.sps_decode(
+    tail = () if static_scratch else (ws.data_ptr(), ws.numel())
+    entry = lib.sps_decode_static if static_scratch else lib.sps_decode
+    status = entry(
         b, h, d, nq,
         q.data_ptr(), _KV_DTYPES[q.dtype], N.i64_array((q.stride(0), q.stride(1), q.stride(2))),
         kv_dtype, len(segments),
@@ -101,9 +106,9 @@ def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor) 
         len(extras), N.ptr_array([t.data_ptr() for t in ek]), N.ptr_array([t.data_ptr() for t in ev]), e_dtype,
         N.i64_array(e_strides), N.i32_array(extra_masks),
         1.0 / math.sqrt(d), out.data_ptr(), N.i64_array((out.stride(0), out.stride(1), out.stride(2))),
-        ws.data_ptr(), ws.numel(), torch.cuda.current_stream(q.device).cuda_stream,
+        *tail, torch.cuda.current_stream(q.device).cuda_stream,
     )
-    N.check("sps_decode", status)
+    N.check("sps_decode_static" if static_scratch else "sps_decode", status)
     return out
 
 
