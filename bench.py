@@ -49,6 +49,13 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def cpu_info() -> dict:
+    import torch
+
+    return {"cpu_count": os.cpu_count(), "threads": torch.get_num_threads(), "model": cpu_model(),
+            "torch": torch.__version__}
+
+
 # ----------------------------------------------------------------------------------------------
 # HBM traffic per launch (from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this script)
 # ----------------------------------------------------------------------------------------------
@@ -156,6 +163,8 @@ def bench_attention(cfg, steps: int, warmup: int):
     dominant = max(kernels, key=lambda name: kernels[name]["ms"])
     dk = kernels[dominant]
     return {
+        "workload": f"{cfg.name}: {cfg.family} attention fwd+bwd, B{cfg.batch} H{cfg.heads} D{cfg.head_dim} "
+                    f"N{cfg.n}" + (f" w={cfg.window}" if cfg.family != "full" else "") + ", packed documents, bf16",
         "value": flops / (ms_per_step * 1e-3) / 1e12,
         "ms_per_step": ms_per_step,
         "device_ms_per_step": statistics.mean(f + a + b for f, a, b in zip(fwd, dq, dkdv)),
@@ -305,10 +314,78 @@ def cpu_attention_baseline(cfg, budget_s: float):
     pairs = visible_pairs(cfg, lengths[:rows]) * cfg.heads
     flops = 14.0 * cfg.head_dim * pairs
     return {"value": round(flops / spent / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", **cpu_info(),
             "sample": f"{rows} of {cfg.batch} batch rows (all {cfg.heads} heads, N={cfg.n}) of the same inputs, "
                       f"dense masked SDPA fwd+bwd fp32 (the reference's test reference), {spent:.1f} s; "
                       f"cpu: {cpu_model()}"}
+
+
+# ----------------------------------------------------------------------------------------------
+# C1: SPS forward at the reference's CPU-runnable size
+# ----------------------------------------------------------------------------------------------
+def bench_c1(cfg, steps: int, cpu: bool):
+    """C1 (SPS forward, B2 H8 D64, 1024 positions, w=64, one document per row, fp32 on the CPU). The
+    reference's CPU paths on this host: (i) its CPU inference path, token by token through
+    masked_kv_attention's padded SDPA (two slots per token over ring ++ retained ++ current keys);
+    (ii) the one-shot dense masked SDPA of its kernel tests. Next to them, the HIP forward on the same
+    inputs cast to bf16 (the kernels compute in bf16 with fp32 accumulation)."""
+    import numpy as np
+    import torch
+
+    from sps_amd import _native as N
+    from sps_amd import attention as SA
+    from sps_amd.workloads import make_qkv, useful_flops
+
+    q, k, v = make_qkv(cfg, seed=0, with_grad=False)
+    lengths = [[cfg.tokens] for _ in range(cfg.batch)]
+    flops = useful_flops(cfg, lengths, bwd=False)
+    scale = 1.0 / math.sqrt(cfg.head_dim)
+    qg, kg, vg = (t.to(torch.bfloat16).cuda() for t in (q, k, v))
+
+    def fwd():
+        SA.attention_forward(qg, kg, vg, scale, N.FAMILY_SPS, cfg.window, None)
+
+    for _ in range(3):
+        fwd()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fwd()
+    e1.record()
+    torch.cuda.synchronize()
+    gpu_us = e0.elapsed_time(e1) * 1e3 / steps
+    out = {"workload": "C1: SPS forward, B2 H8 D64, 1024 positions (512 tokens), w=64, one document per row",
+           "useful_gflop": round(flops / 1e9, 4),
+           "gpu": {"us": round(gpu_us, 2), "tflops": round(flops / (gpu_us * 1e-6) / 1e12, 2), "dtype": "bf16",
+                   "note": "HIP forward on the C1 inputs cast to bf16"}}
+    if cpu:
+        from oracle import cpu_fallback as CF
+
+        def timed(fn, reps):
+            fn()  # warm-up
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            return statistics.median(ts)
+
+        t_step = timed(lambda: CF.stepwise_sps_forward(q, k, v, 1, cfg.window), 3)
+        mask = CF.mask_from_docs(1, np.zeros(cfg.n, dtype=np.int64), cfg.window)
+        bias = torch.zeros(mask.shape)
+        bias.masked_fill_(~mask, float("-inf"))
+        t_dense = timed(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=bias,
+                                                                                  scale=scale), 5)
+        out["cpu_stepwise"] = {"ms": round(t_step * 1e3, 2), "gflops": round(flops / t_step / 1e9, 3),
+                               "dtype": "fp32", "kind": "port", **cpu_info(),
+                               "path": "token by token: masked_kv_attention's padded SDPA, 2 slots x 512 tokens "
+                                       "(reference reverse_sps/inference.py:437-457, decode_attention.py:637-698)"}
+        out["cpu_dense"] = {"ms": round(t_dense * 1e3, 2), "gflops": round(flops / t_dense / 1e9, 3),
+                            "dtype": "fp32", "kind": "port", **cpu_info(),
+                            "path": "one dense masked SDPA over 1024 positions "
+                                    "(reference test_sps_attention.py:25-73)"}
+    return out
 
 
 # ----------------------------------------------------------------------------------------------
@@ -374,6 +451,15 @@ def bench_decode(cfg, steps: int, warmup: int):
         return out
 
     k_us = timed(kernel_call)
+    # The SPS generation step's pair of queries (input and <predict> slots) over the same segments:
+    # one pass over the K/V for both (reverse_sps/inference.py:322-362, triton_segmented_q2_attention).
+    q2 = torch.cat([qd.view(cfg.seqs, 1, cfg.heads, cfg.head_dim)] * 2, dim=1).contiguous()
+    out2 = torch.empty((cfg.seqs, 2, cfg.heads, cfg.head_dim), device=dev, dtype=torch.float32)
+
+    def pair_call():
+        DA._run_decode(q2, 2, segs, ex, [0b11, 0b10], out2)
+
+    q2_us = timed(pair_call)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     a_us = timed(api_call)
@@ -409,11 +495,16 @@ def bench_decode(cfg, steps: int, warmup: int):
     nbytes = decode_bytes(cfg, lengths, nq=1, n_extra=2, kv_bytes=2)
     k_med = statistics.median(k_us)
     gbps = nbytes / (k_med * 1e-6) / 1e9
+    q2_bytes = decode_bytes(cfg, lengths, nq=2, n_extra=2, kv_bytes=2)
+    q2_med = statistics.median(q2_us)
     return {
         "workload": "C5 segmented decode: 64 sequences, 16 heads, D 64, retained U[512,4096] (seed 0), "
                     "ring 64, 1 <predict> query (ring + retained + current input + current <predict>)",
         "us_per_step": round(k_med, 3),
         "api_us_per_step": round(statistics.median(a_us), 3),
+        "q2_us_per_step": round(q2_med, 3),
+        "q2_gbps": round(q2_bytes / (q2_med * 1e-6) / 1e9, 1),
+        "q2_algorithmic_bytes": q2_bytes,
         "kv_update_us": round(statistics.median(u_us), 3),
         "kv_update_gbps": round(upd_bytes / (statistics.median(u_us) * 1e-6) / 1e9, 1),
         "gbps": round(gbps, 1),
@@ -424,6 +515,10 @@ def bench_decode(cfg, steps: int, warmup: int):
                      "traffic": (lambda t: t["decode_partial_kernel"] + t["decode_merge_kernel"]
                                  if "decode_partial_kernel" in t and "decode_merge_kernel" in t else None)(
                                      recorded_traffic())},
+        "kv_update_note": "a launch of its own after the attention (as fused_sps_kv_update is in the reference): "
+                          "the merge kernel reads the ring and retained lengths the update advances, and the "
+                          "ring length is shared by all heads of a sequence, so a fused update would need a "
+                          "grid-wide ordering between the last reader and the writer of each sequence",
         "_api_wall_s": time.perf_counter() - t0,
     }
 
@@ -448,7 +543,7 @@ def cpu_decode_baseline(cfg, budget_s: float):
     med = statistics.median(times)
     nbytes = decode_bytes(cfg, lengths, nq=1, n_extra=2, kv_bytes=2)
     return {"value": round(med * 1e6, 1), "unit": "us/step", "gbps": round(nbytes / med / 1e9, 3),
-            "cores": torch.get_num_threads(), "kind": "port",
+            "cores": torch.get_num_threads(), "kind": "port", **cpu_info(),
             "sample": f"the full C5 step ({len(times)} steps, median) through the reference's padded-SDPA "
                       f"masked_kv_attention fallback in fp32; cpu: {cpu_model()}"}
 
@@ -462,6 +557,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work per baseline leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true", help="skip the C1, C2 and C4 lines")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain streaming kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -482,7 +578,7 @@ def main() -> int:
         print("bench.py needs a GPU (MI355X); none is visible", file=sys.stderr)
         return 1
     from sps_amd import _native
-    from sps_amd.workloads import C3, C5
+    from sps_amd.workloads import C1, C2, C3, C4, C5
 
     _native.lib()
     if args.copy_probe_mib > 0:
@@ -495,6 +591,17 @@ def main() -> int:
     log(f"C3 pre-attention (fused RoPE + casts): {pre}")
     pre["prefill_to_decode"] = bench_prefill_state(C3, 20)
     log(f"C3 prefill -> decode caches: {pre['prefill_to_decode']}")
+    others = {}
+    if not args.no_other_configs:
+        for cfg in (C2, C4):
+            log(f"{cfg.name} fwd+bwd: {args.warmup} warm-up + {args.steps} timed steps")
+            r = bench_attention(cfg, args.steps, args.warmup)
+            r.pop("doc_lengths", None)
+            others[cfg.name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+            log(f"{cfg.name}: {r['value']:.1f} TFLOP/s, {r['ms_per_step']:.3f} ms/step, kernels {r['kernels']}")
+        log("C1 forward (GPU) and the reference's CPU paths")
+        others["C1"] = bench_c1(C1, args.steps, not args.no_cpu_baseline)
+        log(f"C1: {others['C1']}")
     dec = None
     if not args.no_decode:
         log(f"C5 decode: {args.decode_steps} timed steps")
@@ -534,6 +641,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "pre_attention": pre,
         "decode": dec,
+        "configs": others,
     }
     print(json.dumps(line), flush=True)
     return 0

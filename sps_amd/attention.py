@@ -22,7 +22,7 @@ import torch
 
 from . import _native as N
 
-_SUPPORTED_HEAD_DIMS = (16, 32, 64, 128)
+_SUPPORTED_HEAD_DIMS = (16, 32, 64, 128, 256)
 _REFERENCE_HEAD_DIMS = {16, 32, 64, 128, 256}
 
 

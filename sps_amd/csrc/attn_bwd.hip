@@ -27,15 +27,29 @@ namespace sps {
 // Groups of blocks whose loads are in flight while a group is computed (run_groups).
 constexpr int kLook = 1;
 
-// Blocks per barrier (LDS budget: both passes run 2 workgroups per CU, so four 32-row blocks of
-// two tensors, double-buffered, fit; fewer barriers per block than pairs).
-constexpr int kDqGroup = 4;
-constexpr int kDkdvGroup = 4;
+// Blocks per barrier (LDS budget: up to D = 128 both passes run 2 workgroups per CU, so four 32-row
+// blocks of two tensors, double-buffered, fit; fewer barriers per block than pairs). At D = 256 a
+// block is 16 KiB, so groups of two (128 KiB of tiles, one workgroup per CU).
+template <int D>
+constexpr int bwd_group() { return D >= 256 ? 2 : 4; }
+
+// One waves-per-SIMD floor per head dim: 2 at D <= 64; above, the MFMA accumulators of D-wide rows
+// need the registers of one wave per SIMD.
+template <int D>
+constexpr int bwd_waves() { return D <= 64 ? 2 : 1; }
+
+// The wave's own 32-row tile of a [2][NG][32 * D] staging array (an idle buffer at the end of the
+// kernel): every layout holds at least kWaves of them.
+template <int NG, int TE>
+__device__ __forceinline__ uint16_t* wave_tile(uint16_t (&arr)[2][NG][TE], int wave) {
+  static_assert(2 * NG >= kWaves, "one tile per wave");
+  return &arr[0][0][0] + wave * TE;
+}
 
 template <int D, class E>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8))) void attn_bwd_dq_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D>(), 8))) void attn_bwd_dq_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
-  constexpr int NG = kDqGroup;
+  constexpr int NG = bwd_group<D>();
   // Head dims of 128 stage K / V blocks by direct global -> LDS loads into dense swizzled tiles
   // (frees the 64 staging VGPRs: -7 % at D = 128); smaller ones through registers into padded tiles,
   // whose two-group load lookahead measured 3 % faster than the DMA pipeline's one at D = 64.
@@ -260,7 +274,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
   bool staged = false;
   if constexpr (D >= 64) {
     if (rows16_ok(a.dq, a.sdq)) {
-      store_rows_via_lds<D>(sK[0][wave], lane, orow, qvalid, piece);
+      store_rows_via_lds<D>(wave_tile(sK, wave), lane, orow, qvalid, piece);
       staged = true;
     }
   }
@@ -285,9 +299,9 @@ struct ChunkRegs {
 };
 
 template <int D, class E>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2 : 1, 8))) void attn_bwd_dkdv_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D>(), 8))) void attn_bwd_dkdv_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
-  constexpr int NG = kDkdvGroup;
+  constexpr int NG = bwd_group<D>();
   // Head dims of 64 and more stage Q / dO chunks and their seeds by direct global -> LDS loads into
   // dense swizzled tiles; smaller ones through registers into padded tiles.
   constexpr bool kDma = D >= 64;
@@ -514,8 +528,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 2
     if (rows16_ok(a.dk, a.sdk) && rows16_ok(a.dv, a.sdv)) {
       uint16_t* krow = a.dk + b * a.sdk.b + h * a.sdk.h + (int64_t)kp * a.sdk.n;
       uint16_t* vrow = a.dv + b * a.sdv.b + h * a.sdv.h + (int64_t)kp * a.sdv.n;
-      store_rows_via_lds<D>(sQ[0][wave], lane, krow, kvalid, piece_k);
-      store_rows_via_lds<D>(sDO[0][wave], lane, vrow, kvalid, piece_v);
+      store_rows_via_lds<D>(wave_tile(sQ, wave), lane, krow, kvalid, piece_k);
+      store_rows_via_lds<D>(wave_tile(sDO, wave), lane, vrow, kvalid, piece_v);
       staged = true;
     }
   }
@@ -598,6 +612,7 @@ hipError_t launch_attn_bwd(const AttnArgs& a, int D, int is_f16, int passes, hip
     SPS_BWD_CASE(32)
     SPS_BWD_CASE(64)
     SPS_BWD_CASE(128)
+    SPS_BWD_CASE(256)
     default:
       return hipErrorInvalidValue;
   }

@@ -42,7 +42,7 @@ constexpr float kRescaleThreshold = 8.0f;
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
 template <int D, class E>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 2, 8))) void attn_fwd_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : (D <= 128 ? 2 : 1), 8))) void attn_fwd_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
   // Head dims of 64 and more stage K / V blocks by direct global -> LDS loads into dense swizzled
   // tiles (no staging registers, no LDS write instructions); smaller ones through registers into
@@ -361,6 +361,7 @@ hipError_t launch_attn_fwd(const AttnArgs& a, int D, int is_f16, hipStream_t str
     SPS_FWD_CASE(32)
     SPS_FWD_CASE(64)
     SPS_FWD_CASE(128)
+    SPS_FWD_CASE(256)
     default:
       return hipErrorInvalidValue;
   }

@@ -60,7 +60,7 @@ sps::Strides3 strides(const int64_t* st) {
   return s;
 }
 
-bool supported_head_dim(int D) { return D == 16 || D == 32 || D == 64 || D == 128; }
+bool supported_head_dim(int D) { return D == 16 || D == 32 || D == 64 || D == 128 || D == 256; }
 
 struct AttnLayout {
   size_t run_start, run_end, row_mono, q_plan, k_plan, seeds, total;
@@ -400,6 +400,8 @@ static int decode_impl(int B, int H, int D, int nq, const void* q, int q_dtype, 
   a.q_sb = q_strides[0];
   a.q_ss = q_strides[1];
   a.q_sh = q_strides[2];
+  a.q_packed = q_dtype == kv_dtype && kv_dtype != SPS_DTYPE_F32 && aligned16(q) && D % 8 == 0 &&
+               q_strides[0] % 8 == 0 && q_strides[1] % 8 == 0 && q_strides[2] % 8 == 0;
   a.out = out;
   a.o_sb = out_strides[0];
   a.o_ss = out_strides[1];

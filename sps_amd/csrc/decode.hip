@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "cdna4.hpp"
 #include "decode_kernels.hpp"
 
@@ -70,6 +72,25 @@ __device__ __forceinline__ int seg_live_len(const DecodeSeg& sg, int b, int h, i
   return (int)len;
 }
 
+// Sum over aligned groups of W lanes (W <= 16 by DPP moves inside each 16-lane row: quad swaps,
+// then the half-row and row mirrors; every lane of the group receives the sum). Larger groups finish
+// with cross-row shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+template <int W>
+__device__ __forceinline__ float row_group_sum(float x) {
+  if constexpr (W >= 2) x += dpp_f<0xB1>(x);    // quad_perm [1, 0, 3, 2]
+  if constexpr (W >= 4) x += dpp_f<0x4E>(x);    // quad_perm [2, 3, 0, 1]
+  if constexpr (W >= 8) x += dpp_f<0x141>(x);   // row_half_mirror
+  if constexpr (W >= 16) x += dpp_f<0x140>(x);  // row_mirror
+#pragma unroll
+  for (int o = 16; o < W; o <<= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
 template <int W>
 __device__ __forceinline__ float xor_sum(float x) {
 #pragma unroll
@@ -91,7 +112,27 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-template <int D, int NQ, class KV>
+// Packed dot product of 8 16-bit elements (v_dot2_f32_bf16 / v_dot2_f32_f16: exact products,
+// fp32 accumulation) for K/V and query in the same 16-bit type.
+template <class KV>
+__device__ __forceinline__ float dot8_packed(u32x4_t k, u32x4_t q, float acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // Elements copied to scalars first: clang lowers __builtin_bit_cast of a vector-element
+    // subscript (an lvalue) as a read of element 0.
+    const uint32_t ki = k[i], qi = q[i];
+    if constexpr (std::is_same<KV, KvBF16>::value)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, ki), __builtin_bit_cast(bf16x2_t, qi), acc,
+                                           false);
+    else
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, ki), __builtin_bit_cast(f16x2_t, qi), acc, false);
+  }
+  return acc;
+}
+
+// PQ: the query is in the K/V's 16-bit type with 16-byte aligned rows (the host checks), so the
+// scores are packed dot products of raw K words and raw query words, with no conversion of K.
+template <int D, int NQ, class KV, bool PQ>
 __global__ __launch_bounds__(256) void decode_partial_kernel(const DecodeArgs a) {
   constexpr int EPL = 16 / (int)sizeof(typename KV::raw);  // elements per 16-byte load
   constexpr int LPR = D / EPL;                              // lanes per key row
@@ -114,13 +155,18 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const DecodeArgs a)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane / LPR, cc = lane % LPR;
 
-  // This lane's query slice(s): elements cc*EPL .. +EPL.
-  float qv[NQ][EPL];
+  // This lane's query slice(s): elements cc*EPL .. +EPL (fp32, or raw 16-bit words when PQ).
+  float qv[NQ][PQ ? 1 : EPL];
+  u32x4_t qw[NQ];
 #pragma unroll
   for (int qi = 0; qi < NQ; ++qi) {
     const int64_t q0 = b * a.q_sb + qi * a.q_ss + h * a.q_sh + cc * EPL;
+    if constexpr (PQ) {
+      qw[qi] = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(a.q) + q0);
+    } else {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) qv[qi][e] = load_as_f32(a.q, q0 + e, a.q_dtype);
+      for (int e = 0; e < EPL; ++e) qv[qi][e] = load_as_f32(a.q, q0 + e, a.q_dtype);
+    }
   }
 
   using raw_t = typename KV::raw;
@@ -144,14 +190,18 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(const DecodeArgs a)
   float sc[NQ][PASS];
 #pragma unroll
   for (int j = 0; j < PASS; ++j) {
-    float kf[EPL];
-    unpack16<KV>(kr[j], kf);
+    float kf[PQ ? 1 : EPL];
+    if constexpr (!PQ) unpack16<KV>(kr[j], kf);
 #pragma unroll
     for (int qi = 0; qi < NQ; ++qi) {
       float d = 0.f;
+      if constexpr (PQ) {
+        d = dot8_packed<KV>(kr[j], qw[qi], d);
+      } else {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) d = fmaf(qv[qi][e], kf[e], d);
-      d = xor_sum<LPR>(d);
+        for (int e = 0; e < EPL; ++e) d = fmaf(qv[qi][e], kf[e], d);
+      }
+      d = row_group_sum<LPR>(d);
       sc[qi][j] = (tw + j * RPP < live) ? d * a.scale2 : -INFINITY;
     }
   }
@@ -387,8 +437,13 @@ template <int D, int NQ, class KV>
 static hipError_t launch_decode_t(const DecodeArgs& a, hipStream_t stream) {
   if (a.B == 0 || a.H == 0) return hipSuccess;
   if (a.n_chunks > 0) {
-    hipLaunchKernelGGL((decode_partial_kernel<D, NQ, KV>), dim3(a.n_chunks, a.H, a.B), dim3(256), 0,
-                       stream, a);
+    constexpr bool k16 = sizeof(typename KV::raw) == 2;
+    if (k16 && a.q_packed)
+      hipLaunchKernelGGL((decode_partial_kernel<D, NQ, KV, k16>), dim3(a.n_chunks, a.H, a.B), dim3(256), 0,
+                         stream, a);
+    else
+      hipLaunchKernelGGL((decode_partial_kernel<D, NQ, KV, false>), dim3(a.n_chunks, a.H, a.B), dim3(256), 0,
+                         stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -42,6 +42,7 @@ struct DecodeArgs {
   const void* q;  // [B, nq, H, D] of q_dtype (values in the attention dtype), strides (b, slot, h)
   int q_dtype;    // 0 bf16, 1 f16, 2 f32
   int64_t q_sb, q_ss, q_sh;
+  int q_packed;   // q has the K/V's 16-bit dtype, a 16-byte aligned base and strides of 8k elements
   const void* ek[kMaxDecodeExtras];  // extra keys/values [B, H, D] of e_dtype, strides (b, h)
   const void* ev[kMaxDecodeExtras];
   int e_dtype;

@@ -97,6 +97,10 @@ CASES = [
     ("reverse_sps", 2, 2, 512, 64, 64, "packed", None, torch.bfloat16, "bhnd"),
     ("reverse_sps", 1, 2, 340, 128, 17, None, 40, torch.float16, "bnhd"),
     ("reverse_sps", 1, 1, 200, 64, -1, "packed", None, torch.bfloat16, "bhnd"),
+    # head dim 256 (accepted by the reference's prefill asserts, triton_sps_flash_attention.py:510)
+    ("full", 1, 2, 300, 256, 0, "packed", None, torch.bfloat16, "bhnd"),
+    ("sps", 1, 2, 320, 256, 17, "packed", None, torch.float16, "bnhd"),
+    ("reverse_sps", 2, 1, 260, 256, 64, None, 5, torch.bfloat16, "bhnd"),
 ]
 
 
@@ -373,3 +377,16 @@ def test_any_sm_scale(family, sm_scale):
     # scaled scores, so a zero scale gives the mean of the visible values and a negative one flips
     # the scores.
     _scaled_check(family, 256, 64, 1.0, torch.bfloat16, window=5, sm_scale=sm_scale, seed=3)
+
+
+def test_c1_shape_forward_against_oracle():
+    # C1 (SPS forward, B2 H8 D64, 512 tokens -> 1024 positions, w=64, one document per row; fp32 on
+    # the reference's CPU path): the same seeded inputs cast to bf16 through the HIP forward, every
+    # (batch, head) against the oracle on the rounded inputs.
+    from sps_amd.workloads import C1, make_qkv
+
+    q, k, v = (t.to(torch.bfloat16) for t in make_qkv(C1, seed=0, with_grad=False))
+    out = SA.sps_sliding_attention(q.cuda(), k.cuda(), v.cuda(), 1 / math.sqrt(C1.head_dim), C1.window)
+    mask = M.batch_mask(N.FAMILY_SPS, None, n=C1.n, window=C1.window, batch=C1.batch)
+    o_ref, _ = A.forward(q.float().numpy(), k.float().numpy(), v.float().numpy(), mask, 1 / math.sqrt(C1.head_dim))
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(o_ref).float(), atol=ATOL, rtol=RTOL)
