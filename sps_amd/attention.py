@@ -122,6 +122,26 @@ def attention_forward(q, k, v, sm_scale, family, window=0, documents_idx_BxT=Non
     return o, lse, q, k, v, (ws if keep else None)
 
 
+def backward_pass_args(do, q, k, v, o, lse, dq, dk, dv, sm_scale, family, window=0, documents_idx_BxT=None,
+                       persistent_key_window=None, workspace=None):
+    """The argument tuple of sps_attn_bwd_pass after its `pass` argument, for callers that launch the
+    passes themselves (q, k, v, do as the kernels read them; dq, dk, dv allocated like q, k, v)."""
+    b, h, n, d = q.shape
+    docs_ptr, docs_code, docs_sb = _docs_args(documents_idx_BxT)
+    ws = workspace if workspace is not None else _workspace(family, b, h, n, documents_idx_BxT is not None, True,
+                                                            q.device)
+    has_pkw = persistent_key_window is not None
+    return (
+        family, b, h, n, d, _dtype_code(q),
+        q.data_ptr(), _strides(q), k.data_ptr(), _strides(k), v.data_ptr(), _strides(v),
+        o.data_ptr(), _strides(o), do.data_ptr(), _strides(do), lse.data_ptr(),
+        dq.data_ptr(), _strides(dq), dk.data_ptr(), _strides(dk), dv.data_ptr(), _strides(dv),
+        docs_ptr, docs_code, docs_sb,
+        float(sm_scale), int(window), int(has_pkw), int(persistent_key_window) if has_pkw else -1,
+        ws.data_ptr(), ws.numel(), _stream(q),
+    ), ws
+
+
 def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, documents_idx_BxT=None,
                        persistent_key_window=None, between_passes=None, layout_workspace=None):
     """Runs the backward kernels; returns (dq, dk, dv) laid out like q, k, v.
@@ -132,23 +152,12 @@ def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, document
     ``attention_forward(keep_layout=True)`` for the same arguments; the backward then reuses its
     document layout instead of recomputing it."""
     do = _kernel_view(do)
-    b, h, n, d = q.shape
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    docs_ptr, docs_code, docs_sb = _docs_args(documents_idx_BxT)
     reuse = layout_workspace is not None and documents_idx_BxT is not None
-    ws = layout_workspace if reuse else _workspace(family, b, h, n, documents_idx_BxT is not None, True, q.device)
-    has_pkw = persistent_key_window is not None
-    args = (
-        family, b, h, n, d, _dtype_code(q),
-        q.data_ptr(), _strides(q), k.data_ptr(), _strides(k), v.data_ptr(), _strides(v),
-        o.data_ptr(), _strides(o), do.data_ptr(), _strides(do), lse.data_ptr(),
-        dq.data_ptr(), _strides(dq), dk.data_ptr(), _strides(dk), dv.data_ptr(), _strides(dv),
-        docs_ptr, docs_code, docs_sb,
-        float(sm_scale), int(window), int(has_pkw), int(persistent_key_window) if has_pkw else -1,
-        ws.data_ptr(), ws.numel(), _stream(q),
-    )
+    args, ws = backward_pass_args(do, q, k, v, o, lse, dq, dk, dv, sm_scale, family, window, documents_idx_BxT,
+                                  persistent_key_window, layout_workspace if reuse else None)
     lib = N.lib()
     reuse_bit = N.BWD_REUSE_LAYOUT if reuse else 0
     if between_passes is None:

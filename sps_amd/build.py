@@ -38,6 +38,15 @@ HIP_FLAGS = [
 
 SOURCES = ["attn_prep.hip", "attn_fwd.hip", "attn_bwd.hip", "decode.hip", "kv_update.hip", "rope.hip", "prefill_state.hip", "doc_ids.hip", "capi.cpp"]
 
+# Per-source flags. The attention kernels are scheduled with LLVM's iterative ILP strategy, which
+# interleaves their MFMA, exponential and LDS work more densely than the default occupancy-driven
+# scheduler at the same register budget (measured on MI355X: C4 (D = 128) fwd+bwd -15 %, C3 (D = 64)
+# unchanged).
+SOURCE_FLAGS = {
+    "attn_fwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    "attn_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+}
+
 
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
@@ -47,7 +56,7 @@ def _hipcc() -> str:
 
 
 def _compile(hipcc: str, src: Path, obj: Path) -> None:
-    cmd = [hipcc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIP_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
