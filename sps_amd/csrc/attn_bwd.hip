@@ -50,10 +50,10 @@ template <int D, class E>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D>(), 8))) void attn_bwd_dq_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
   constexpr int NG = bwd_group<D>();
-  // Head dims of 128 stage K / V blocks by direct global -> LDS loads into dense swizzled tiles
-  // (frees the 64 staging VGPRs: -7 % at D = 128); smaller ones through registers into padded tiles,
-  // whose two-group load lookahead measured 3 % faster than the DMA pipeline's one at D = 64.
-  constexpr bool kDma = D >= 128;
+  // Head dims of 64 and more stage K / V blocks by direct global -> LDS loads into dense swizzled
+  // tiles (frees the staging VGPRs: -7 % at D = 128, -2 % of the C3 step at D = 64 under the
+  // iterative ILP schedule); smaller ones through registers into padded tiles.
+  constexpr bool kDma = D >= 64;
   using DT = DmaTile<kDma ? D : 64>;
   constexpr int TE = kDma ? DT::ELEMS : G::ELEMS;
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][NG][TE];  // [buffer][block of the group]
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
     auto cls_of = [&](int i) {
       return classify_block(i < plan.n0 ? st.w0 : st.w1, plan.first(i), EXACT);
     };
-    const BlockMask bm = build_block_mask(nb, cls_of);
+    const BlockMask bm = q_block_mask(st, EXACT);
     auto body = [&](int j, int buf) {
       int act2, full2;
       group_codes<NG>(bm, NG * j, nb, cls_of, act2, full2);
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
     // one FMA per score with the -LSE seeds (S * scale2 - LSE), never by rounding a scaled K.
     const float scale2 = a.scale2;
     auto cls_of = [&](int i) { return classify_block(st.w, (st.c0 + i) * kBlock, EXACT); };
-    const BlockMask bm = build_block_mask(nc, cls_of);
+    const BlockMask bm = k_block_mask(st, EXACT);
     auto body = [&](int j, int buf) {
       int act2, full2;
       group_codes<NG>(bm, NG * j, nc, cls_of, act2, full2);
@@ -565,9 +565,10 @@ __global__ __launch_bounds__(256) void mask_dump_kv_kernel(const AttnArgs a) {
   if (k_begin(a, tp, row, s_span, st, run_end)) k_lanes(m, run_end, st);
   const bool exact = row.mono;
   const int64_t dk_doc = (!exact && st.kvalid) ? load_doc(a, b, st.kp) : 0;
+  const BlockMask bm = k_block_mask(st, exact);
   for (int i = 0; i < st.nc; ++i) {
     const int qc = (st.c0 + i) * kBlock;
-    const int cls = classify_block(st.w, qc, exact);
+    const int cls = i < 128 ? mask_class(bm, i) : classify_block(st.w, qc, exact);
     if (cls == TILE_SKIP || !st.kvalid) continue;
     uint32_t bits = 0xffffu;
     if (cls == TILE_PARTIAL) {

@@ -186,7 +186,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
     auto cls_of = [&](int i) {
       return classify_block(i < plan.n0 ? st.w0 : st.w1, plan.first(i), EXACT);
     };
-    const BlockMask bm = build_block_mask(nb, cls_of);
+    const BlockMask bm = q_block_mask(st, EXACT);
     auto body = [&](int j, int buf) {
       int act2, full2;
       pair_codes(bm, 2 * j, nb, cls_of, act2, full2);
@@ -320,12 +320,13 @@ __global__ __launch_bounds__(256) void mask_dump_q_kernel(const AttnArgs a) {
   const bool exact = row.mono;
   const int64_t dq_doc = (!exact && qvalid) ? load_doc(a, b, qp) : 0;
   uint8_t* mrow = a.mask_out + ((int64_t)b * m.N + (qvalid ? qp : 0)) * m.N;
+  const BlockMask bm = q_block_mask(st, exact);
   for (int i = 0; i < plan.count(); ++i) {
     const bool s0 = i < plan.n0;
     const int t0 = plan.first(i), stream = plan.stream(i);
     const WaveSpan ws = s0 ? st.w0 : st.w1;
     const Interval lr = s0 ? st.r0 : st.r1;
-    const int cls = classify_block(ws, t0, exact);
+    const int cls = i < 128 ? mask_class(bm, i) : classify_block(ws, t0, exact);
     if (cls == TILE_SKIP || !qvalid) continue;
     uint32_t bits = 0xffffu;
     if (cls == TILE_PARTIAL) {

@@ -150,7 +150,7 @@ __device__ __forceinline__ WaveSpan wave_span(const Interval& r) {
 
 // Class of the block of 32 indices [t0, t0 + 31] for a wave. `exact_docs` is false when the row's
 // ids are not a sequence of runs (then every visible-by-interval pair still needs an id check).
-__device__ __forceinline__ int classify_block(const WaveSpan& w, int t0, bool exact_docs) {
+__host__ __device__ __forceinline__ int classify_block(const WaveSpan& w, int t0, bool exact_docs) {
   if (t0 > w.max_hi || t0 + kBlock - 1 < w.min_lo) return TILE_SKIP;
   if (exact_docs && t0 >= w.max_lo && t0 + kBlock - 1 <= w.min_hi) return TILE_FULL;
   return TILE_PARTIAL;

@@ -388,29 +388,64 @@ __device__ __forceinline__ void k_workgroup(const AttnArgs& a, int& b, int& h, T
 
 
 // Per-wave classes of the first 128 blocks of a loop as bitmasks (bit i: block i is not SKIP / is
-// FULL for this wave), built once, so the loops test two bits per pair of blocks instead of
-// re-deriving streams, spans and classes. Blocks from 128 on are classified on the fly.
+// FULL for this wave), so the loops test two bits per pair of blocks instead of re-deriving streams,
+// spans and classes. Blocks from 128 on are classified on the fly.
 struct BlockMask {
   uint64_t act0, act1, full0, full1;  // blocks 0..63 and 64..127 (separate words: no dynamic indexing)
 };
 
-template <class ClassFn>
-__device__ __forceinline__ BlockMask build_block_mask(int nb, ClassFn cls_of) {
-  BlockMask bm = {0ull, 0ull, 0ull, 0ull};
-  const int n = imin(nb, 128);
-  for (int i = 0; i < n; ++i) {
-    const int c = cls_of(i);
-    const uint64_t bit = 1ull << (i & 63);
-    const uint64_t a = c != TILE_SKIP ? bit : 0ull, f = c == TILE_FULL ? bit : 0ull;
-    if (i < 64) {
-      bm.act0 |= a;
-      bm.full0 |= f;
-    } else {
-      bm.act1 |= a;
-      bm.full1 |= f;
-    }
+// Bits [lo, hi] (inclusive; none when lo > hi) of the 64-bit word that holds bits [base, base + 63].
+__host__ __device__ __forceinline__ uint64_t bit_range64(int lo, int hi, int base) {
+  const int l = imax(lo - base, 0), h = imin(hi - base, 63);
+  return l > h ? 0ull : ((~0ull >> (63 - imax(h, 0))) & (~0ull << imin(l, 63)));
+}
+
+__host__ __device__ __forceinline__ void set_range(uint64_t& w0, uint64_t& w1, int lo, int hi) {
+  w0 |= bit_range64(lo, hi, 0);
+  w1 |= bit_range64(lo, hi, 64);
+}
+
+// Adds the classes of loop blocks [i0, i0 + n), which hold the 32-row blocks bfirst, bfirst + 1, ...
+// of one stream, for a wave with span w: exactly classify_block's classes in closed form. A block
+// b (rows [32 b, 32 b + 31]) is not SKIP iff 32 b <= max_hi and 32 b + 31 >= min_lo, i.e. b in
+// [min_lo / 32, max_hi / 32] (bounds of non-empty intervals are >= 0), and FULL iff 32 b >= max_lo
+// and 32 b + 31 <= min_hi, i.e. b in [ceil(max_lo / 32), floor((min_hi + 1) / 32) - 1]; both are
+// contiguous ranges, so the masks are two bit ranges instead of a loop over the blocks.
+__host__ __device__ __forceinline__ void add_block_classes(BlockMask& bm, const WaveSpan& w, bool exact, int i0, int n,
+                                                  int bfirst) {
+  if (n <= 0) return;
+  const int last = i0 + n - 1;
+  if (w.min_lo <= w.max_hi) {
+    const int lo = imax((w.min_lo >> 5) - bfirst + i0, i0), hi = imin((w.max_hi >> 5) - bfirst + i0, last);
+    set_range(bm.act0, bm.act1, lo, hi);
   }
+  if (exact && w.max_lo <= w.min_hi) {
+    const int lo = imax(((w.max_lo + 31) >> 5) - bfirst + i0, i0);
+    const int hi = imin(((w.min_hi + 1) >> 5) - 1 - bfirst + i0, last);
+    set_range(bm.full0, bm.full1, lo, hi);
+  }
+}
+
+// Masks of a query-stationary plan (stream-0 blocks, then temporary-stream blocks).
+__device__ __forceinline__ BlockMask q_block_mask(const QState& st, bool exact) {
+  BlockMask bm = {0ull, 0ull, 0ull, 0ull};
+  add_block_classes(bm, st.w0, exact, 0, st.plan.n0, st.plan.b0);
+  add_block_classes(bm, st.w1, exact, st.plan.n0, st.plan.n1, st.plan.b1);
   return bm;
+}
+
+// Masks of a key-stationary plan (query chunks c0, c0 + 1, ...).
+__device__ __forceinline__ BlockMask k_block_mask(const KState& st, bool exact) {
+  BlockMask bm = {0ull, 0ull, 0ull, 0ull};
+  add_block_classes(bm, st.w, exact, 0, st.nc, st.c0);
+  return bm;
+}
+
+// Class of block i (< 128) from the masks.
+__host__ __device__ __forceinline__ int mask_class(const BlockMask& bm, int i) {
+  const uint64_t a = i < 64 ? bm.act0 : bm.act1, f = i < 64 ? bm.full0 : bm.full1;
+  const int sh = i & 63;
+  return ((a >> sh) & 1ull) ? (((f >> sh) & 1ull) ? TILE_FULL : TILE_PARTIAL) : TILE_SKIP;
 }
 
 // G-bit activity and fullness codes of blocks i .. i + G - 1 (i a multiple of G, G a power of two

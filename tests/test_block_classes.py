@@ -1,0 +1,23 @@
+"""The attention kernels classify key blocks (SKIP / PARTIAL / FULL) per wave from closed-form bit
+ranges; this builds the host check of tests/native/block_classes_check.hip, which compares them
+with the per-block predicate on random spans and plans, and runs it on the CPU."""
+
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+HERE = Path(__file__).resolve().parent
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(),
+                    reason="hipcc not available")
+def test_closed_form_block_classes(tmp_path):
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    exe = tmp_path / "block_classes_check"
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-O2", "-std=c++17", "-w",
+                    str(HERE / "native" / "block_classes_check.hip"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe), "200000"], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert out.stdout.strip().endswith("bad 0")
