@@ -121,7 +121,7 @@ def recorded_traffic() -> dict:
 # ----------------------------------------------------------------------------------------------
 # Prefill / training: C3
 # ----------------------------------------------------------------------------------------------
-def bench_attention(cfg, steps: int, warmup: int):
+def bench_attention(cfg, steps: int, warmup: int, traffic: bool = False):
     import torch
 
     from sps_amd import _native as N
@@ -211,7 +211,8 @@ def bench_attention(cfg, steps: int, warmup: int):
                            "algorithmic_gflop": round(x["flop"] / 1e9, 3)} for name, x in kernels.items()},
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(dk["tflops"], 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dk["frac"], 4),
-                     "traffic": recorded_traffic().get(dominant)},
+                     # The recorded traffic is of the C3 workload's launches.
+                     "traffic": recorded_traffic().get(dominant) if traffic else None},
     }
 
 
@@ -342,20 +343,23 @@ def cpu_attention_baseline(cfg, budget_s: float):
     n_w = 256
     CF.dense_sdpa_fwd_bwd(q[:1, :, :n_w], k[:1, :, :n_w], v[:1, :, :n_w], do[:1, :, :n_w],
                           CF.mask_from_docs(family, ids[0, :n_w], cfg.window).unsqueeze(0), scale)
-    rows, spent = 0, 0.0
-    while rows < cfg.batch and (rows == 0 or spent < budget_s):
-        mask = CF.mask_from_docs(family, ids[rows], cfg.window).unsqueeze(0)
+    # Rows in order, cycling over the batch, until the budget is spent (at least one row, at most 8
+    # passes over the batch).
+    done, spent, pairs = 0, 0.0, 0
+    while done < 8 * cfg.batch and (done == 0 or spent < budget_s):
+        r = done % cfg.batch
+        mask = CF.mask_from_docs(family, ids[r], cfg.window).unsqueeze(0)
         t0 = time.perf_counter()
-        CF.dense_sdpa_fwd_bwd(q[rows:rows + 1], k[rows:rows + 1], v[rows:rows + 1], do[rows:rows + 1], mask, scale)
+        CF.dense_sdpa_fwd_bwd(q[r:r + 1], k[r:r + 1], v[r:r + 1], do[r:r + 1], mask, scale)
         spent += time.perf_counter() - t0
-        rows += 1
-    pairs = visible_pairs(cfg, lengths[:rows]) * cfg.heads
+        pairs += visible_pairs(cfg, lengths[r:r + 1]) * cfg.heads
+        done += 1
     flops = 14.0 * cfg.head_dim * pairs
     return {"value": round(flops / spent / 1e12, 6), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port", **cpu_info(),
-            "sample": f"{rows} of {cfg.batch} batch rows (all {cfg.heads} heads, N={cfg.n}) of the same inputs, "
-                      f"dense masked SDPA fwd+bwd fp32 (the reference's test reference), {spent:.1f} s; "
-                      f"cpu: {cpu_model()}"}
+            "sample": f"{done} batch rows ({done / cfg.batch:g} passes over the {cfg.batch} rows; all {cfg.heads} "
+                      f"heads, N={cfg.n}) of the same inputs, dense masked SDPA fwd+bwd fp32 (the reference's "
+                      f"test reference), {spent:.1f} s; cpu: {cpu_model()}"}
 
 
 # ----------------------------------------------------------------------------------------------
@@ -598,6 +602,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true", help="skip the C1, C2 and C4 lines")
+    ap.add_argument("--profile-config", choices=("C2", "C3", "C4"),
+                    help="run only this configuration's fwd+bwd steps and print its kernel timings (for profilers)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a plain streaming kernel over this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -621,11 +627,18 @@ def main() -> int:
     from sps_amd.workloads import C1, C2, C3, C4, C5
 
     _native.lib()
+    if args.profile_config:
+        cfg = {"C2": C2, "C3": C3, "C4": C4}[args.profile_config]
+        log(f"{cfg.name} fwd+bwd only: {args.warmup} warm-up + {args.steps} timed steps")
+        r = bench_attention(cfg, args.steps, args.warmup)
+        print(json.dumps({"config": cfg.name, "value": round(r["value"], 3), "unit": "TFLOP/s",
+                          "ms_per_step": round(r["ms_per_step"], 4), "kernels": r["kernels"]}), flush=True)
+        return 0
     if args.copy_probe_mib > 0:
         log(f"copy probe: torch.neg over {args.copy_probe_mib} MiB fp32, 3 launches")
         copy_probe(args.copy_probe_mib)
     log(f"C3 fwd+bwd: {args.warmup} warm-up + {args.steps} timed steps")
-    att = bench_attention(C3, args.steps, args.warmup)
+    att = bench_attention(C3, args.steps, args.warmup, traffic=True)
     log(f"C3: {att['value']:.1f} TFLOP/s, {att['ms_per_step']:.3f} ms/step, kernels {att['kernels']}")
     pre = bench_pre_attention(C3, 20)
     log(f"C3 pre-attention (fused RoPE + casts): {pre}")
