@@ -83,14 +83,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
   const auto k_off = TileRegs<D>::offsets(tid, (uint32_t)(step * a.sk.n * 2));
   const auto v_off = TileRegs<D>::offsets(tid, (uint32_t)(step * a.sv.n * 2));
 
+  // Scores are masked (-inf) before they are scaled, and the pair's max is taken over the raw
+  // scores, so the scale must be positive: a negative sm_scale flips the sign of Q instead (exact in
+  // bf16/f16: S * scale2 = (-S) * (-scale2)), and a zero one becomes 2^-100 (every visible score
+  // scales to within 2^-80 of 0, as with scale 0, while masked ones stay -inf).
+  const bool flip_q = a.scale2 < 0.f;
+  const float scale2 = flip_q ? -a.scale2 : (a.scale2 == 0.f ? 0x1p-100f : a.scale2);
+
   // Q fragments: B operand of S^T = K Q^T (lane: query c32, d = 16c + 8g .. +7).
   u32x4_t qf[D / 16];
   {
     const uint16_t* qrow = a.q + b * a.sq.b + h * a.sq.h + (int64_t)(qvalid ? qp : 0) * a.sq.n;
+    const uint32_t sign = flip_q ? 0x80008000u : 0u;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
       u32x4_t z = {0u, 0u, 0u, 0u};
       qf[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(qrow + 16 * c + 8 * g) : z;
+      qf[c] ^= sign;
     }
   }
 
@@ -166,12 +175,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
     if (nb > 0) issue_dma(0, 0);
 
   if (planned) q_lanes(m, qp, run_start, st);
-  const float scale2 = a.scale2;
   float negm = 0.f;  // -m_run (0 while no score has been seen): the per-score FMA subtracts m_run
-
-  // The pair's max (relative to m_run) must exceed thr to raise m_run: any score while none has been
-  // seen, then the lazy-rescale threshold.
-  float thr = -INFINITY;
   float m_run = -INFINITY, l_run[4] = {0.f, 0.f, 0.f, 0.f};
   f32x16_t acc[G::DC];
 #pragma unroll
@@ -199,12 +203,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
 #pragma unroll
         for (int c = 1; c < D / 16; ++c) sc[y] = E::mfma(row_frag(kt, c), qf[c], sc[y]);
       }
-      // Scaled scores relative to the running max: S * scale2 - m_run, in fp32.
-#pragma unroll
-      for (int y = 0; y < 2; ++y) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sc[y][e] = __builtin_fmaf(sc[y][e], scale2, negm);
-      }
       if (full2 != 3) {
 #pragma unroll
         for (int y = 0; y < 2; ++y) {
@@ -220,21 +218,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
           }
         }
       }
-      // The pair's max relative to the running max.
-      const float mb = half_max(max32(sc[0], sc[1]));
-      const bool need = mb > thr;
+      // The pair's max in scaled units (the max of the raw scores, times scale2 > 0). m_run is
+      // raised only past the lazy-rescale threshold (any score while none has been seen); the scores
+      // themselves stay raw, so a rescale touches only the accumulators, and they are scaled below
+      // by one FMA each, S * scale2 - m_run, in fp32.
+      const float mb = half_max(max32(sc[0], sc[1])) * scale2;
+      const bool need = m_run == -INFINITY ? mb > -INFINITY : mb - m_run > kRescaleThreshold;
       if (wave_any(need)) {
-        const float m_new = need ? (m_run == -INFINITY ? mb : m_run + mb) : m_run;
+        const float m_new = need ? mb : m_run;
         const float alpha = need ? fast_exp2(m_run - m_new) : 1.f;
-        const float sh = need ? mb : 0.f;
         m_run = m_new;
-        thr = m_run == -INFINITY ? -INFINITY : kRescaleThreshold;
 #pragma unroll
         for (int r = 0; r < 4; ++r) l_run[r] *= alpha;
 #pragma unroll
         for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
-#pragma unroll
-        for (int y = 0; y < 2; ++y) sc[y] -= sh;
         negm = m_run == -INFINITY ? 0.f : -m_run;
       }
 #pragma unroll
@@ -242,8 +239,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
         uint32_t pk[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float p0 = fast_exp2(sc[y][2 * e]);
-          const float p1 = fast_exp2(sc[y][2 * e + 1]);
+          const float p0 = fast_exp2(__builtin_fmaf(sc[y][2 * e], scale2, negm));
+          const float p1 = fast_exp2(__builtin_fmaf(sc[y][2 * e + 1], scale2, negm));
           pk[e] = E::pack2(p0, p1);
           l_run[e & 3] = E::sum2(pk[e], l_run[e & 3]);  // four independent partial sums
         }
