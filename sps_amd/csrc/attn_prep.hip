@@ -88,29 +88,62 @@ __device__ void k_tile_plan(const MaskSpec& m, const RunBounds& rb, int kt, int&
 }
 
 // Exclusive scans of the per-thread chunk summaries, both in one pass so their latencies overlap:
-// a max-scan of `up` in thread order and a min-scan of `down` in reverse thread order (a shuffle
-// scan inside each wave, then the waves' totals through LDS; two barriers in all).
+// a max-scan of `up` in thread order and a min-scan of `down` in reverse thread order. Inside each
+// wave: DPP shifts within the 16-lane rows (no LDS round trips), then the rows' totals from one lane
+// each; across the waves: their totals through LDS, read back as vectors (two barriers in all).
 constexpr int kPrepWaves = kPrepThreads / 64;
+static_assert(kPrepWaves == 16, "the wave totals are read back as four int4 vectors");
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_shift(int x, int id) {
+  // Lanes whose source lane lies outside the shift's range get `id`.
+  return __builtin_amdgcn_update_dpp(id, x, CTRL, 0xF, 0xF, false);
+}
 
 __device__ void block_exclusive_scans(int* s_up, int* s_down, int up, int down, int up_identity, int down_identity,
                                       int& up_ex, int& down_ex) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int u = up, d = down;  // inclusive scans within the wave
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int yu = __shfl_up(u, o), yd = __shfl_down(d, o);
-    if (lane >= o) u = imax(u, yu);
-    if (lane + o < 64) d = imin(d, yd);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = lane >> 4;
+  const int iu = up_identity, id = down_identity;
+  // Inclusive max-scan upward (row_shr 1, 2, 4, 8) and min-scan downward (row_shl 1, 2, 4, 8) per row.
+  int u = up, d = down;
+  u = imax(u, dpp_shift<0x111>(u, iu));
+  d = imin(d, dpp_shift<0x101>(d, id));
+  u = imax(u, dpp_shift<0x112>(u, iu));
+  d = imin(d, dpp_shift<0x102>(d, id));
+  u = imax(u, dpp_shift<0x114>(u, iu));
+  d = imin(d, dpp_shift<0x104>(d, id));
+  u = imax(u, dpp_shift<0x118>(u, iu));
+  d = imin(d, dpp_shift<0x108>(d, id));
+  // Across the rows: row r adds the totals of rows below it (up) / above it (down).
+  const int t0 = __builtin_amdgcn_readlane(u, 15), t1 = __builtin_amdgcn_readlane(u, 31);
+  const int t2 = __builtin_amdgcn_readlane(u, 47), t3 = __builtin_amdgcn_readlane(u, 63);
+  const int p1 = t0, p2 = imax(t0, t1), p3 = imax(p2, t2);
+  u = imax(u, row == 0 ? iu : row == 1 ? p1 : row == 2 ? p2 : p3);
+  const int b0 = __builtin_amdgcn_readlane(d, 0), b1 = __builtin_amdgcn_readlane(d, 16);
+  const int b2 = __builtin_amdgcn_readlane(d, 32), b3 = __builtin_amdgcn_readlane(d, 48);
+  const int s2 = b3, s1 = imin(b2, b3), s0 = imin(b1, s1);
+  d = imin(d, row == 3 ? id : row == 2 ? s2 : row == 1 ? s1 : s0);
+  if (lane == 0) {
+    s_up[wave] = imax(p3, t3);
+    s_down[wave] = imin(b0, s0);
   }
-  if (lane == 63) s_up[wave] = u;
-  if (lane == 0) s_down[kPrepWaves - 1 - wave] = d;
+  // The lane's exclusive value inside the wave: its neighbour's inclusive one (wave_shr / wave_shl 1).
+  const int eu = dpp_shift<0x138>(u, iu), ed = dpp_shift<0x130>(d, id);
   __syncthreads();
-  int cu = up_identity, cd = down_identity;
-  for (int w = 0; w < wave; ++w) cu = imax(cu, s_up[w]);
-  for (int w = 0; w < kPrepWaves - 1 - wave; ++w) cd = imin(cd, s_down[w]);
-  int eu = __shfl_up(u, 1), ed = __shfl_down(d, 1);
-  if (lane == 0) eu = up_identity;
-  if (lane == 63) ed = down_identity;
+  int cu = iu, cd = id;
+#pragma unroll
+  for (int k = 0; k < kPrepWaves / 4; ++k) {
+    const int4 vu = reinterpret_cast<const int4*>(s_up)[k], vd = reinterpret_cast<const int4*>(s_down)[k];
+    const int w = 4 * k;
+    cu = imax(cu, w + 0 < wave ? vu.x : iu);
+    cu = imax(cu, w + 1 < wave ? vu.y : iu);
+    cu = imax(cu, w + 2 < wave ? vu.z : iu);
+    cu = imax(cu, w + 3 < wave ? vu.w : iu);
+    cd = imin(cd, w + 0 > wave ? vd.x : id);
+    cd = imin(cd, w + 1 > wave ? vd.y : id);
+    cd = imin(cd, w + 2 > wave ? vd.z : id);
+    cd = imin(cd, w + 3 > wave ? vd.w : id);
+  }
   __syncthreads();  // the wave totals may be overwritten by a later scan
   up_ex = imax(cu, eu);
   down_ex = imin(cd, ed);
@@ -139,7 +172,7 @@ __device__ void sort_tiles(const int* cost, int n, int first, int count, Emit em
 }
 
 __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs a) {
-  __shared__ int s_scan[kPrepThreads];
+  __shared__ __attribute__((aligned(16))) int s_scan[kPrepThreads];
   __shared__ int s_cost[kMaxSortTiles], s_cost_k[kMaxSortTiles];
   __shared__ int s_qplan[kMaxSortTiles][4], s_kplan[kMaxSortTiles][2];
   __shared__ int s_nonmono;
@@ -232,21 +265,6 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   }
   if (tid == 0) a.row_mono[b] = mono ? 1 : 0;
   __syncthreads();  // start/end of the whole row are visible to every thread below
-  if (in_regs) {
-    // Rows held in LDS: one pass of consecutive positions per thread group, 4 per thread (16-byte
-    // stores) when the row length allows.
-    if ((N & 3) == 0) {
-      for (int p = 4 * tid; p < N; p += 4 * kPrepThreads) {
-        *reinterpret_cast<int4*>(start + p) = make_int4(s_start[p], s_start[p + 1], s_start[p + 2], s_start[p + 3]);
-        *reinterpret_cast<int4*>(end + p) = make_int4(s_end[p], s_end[p + 1], s_end[p + 2], s_end[p + 3]);
-      }
-    } else {
-      for (int p = tid; p < N; p += kPrepThreads) {
-        start[p] = s_start[p];
-        end[p] = s_end[p];
-      }
-    }
-  }
   // Rows that fit read their run bounds from LDS (short: positions < kLdsRow <= 32767).
   const bool lds_ok = in_regs;
   const RunBounds rb = {lds_ok ? s_start : nullptr, lds_ok ? s_end : nullptr, start, end};
@@ -302,6 +320,22 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
     sort_tiles(s_cost_k, nkt, kPrepThreads / 2, kPrepThreads / 2, [&](int r, int t) {
       kplan[r] = TilePlan{t, mono_flag, s_kplan[t][0], s_kplan[t][1], 0, 0, 0, 0};
     });
+  if (in_regs) {
+    // Rows held in LDS reach global memory last, so no barrier above waits for these stores: one
+    // pass of consecutive positions per thread group, 4 per thread (16-byte stores) when the row
+    // length allows.
+    if ((N & 3) == 0) {
+      for (int p = 4 * tid; p < N; p += 4 * kPrepThreads) {
+        *reinterpret_cast<int4*>(start + p) = make_int4(s_start[p], s_start[p + 1], s_start[p + 2], s_start[p + 3]);
+        *reinterpret_cast<int4*>(end + p) = make_int4(s_end[p], s_end[p + 1], s_end[p + 2], s_end[p + 3]);
+      }
+    } else {
+      for (int p = tid; p < N; p += kPrepThreads) {
+        start[p] = s_start[p];
+        end[p] = s_end[p];
+      }
+    }
+  }
 }
 
 hipError_t launch_row_layout(const AttnArgs& a, hipStream_t stream) {
