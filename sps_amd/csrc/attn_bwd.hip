@@ -38,6 +38,22 @@ constexpr int bwd_group() { return D >= 256 ? 2 : 4; }
 template <int D>
 constexpr int bwd_waves() { return D <= 64 ? 2 : 1; }
 
+// The dQ pass at D = 64 runs 3 waves per SIMD instead: groups of two blocks (32 KiB of tiles, so the
+// LDS holds three workgroups per CU) and 168 VGPRs (dQ -4 % at C3, -6 % at C2 against four-block
+// groups at 2 waves per SIMD).
+template <int D>
+constexpr int dq_group() { return D == 64 ? 2 : bwd_group<D>(); }
+template <int D>
+constexpr int dq_waves() { return D == 64 ? 3 : bwd_waves<D>(); }
+
+// The wave index, wave-uniform at D = 64 (so every LDS address derived from it, the direct-to-LDS
+// loads' M0 values among them, is computed in scalar registers instead of VGPRs that the 3-wave dQ
+// pass would have to spill).
+template <int D>
+__device__ __forceinline__ int wave_index() {
+  return D == 64 ? wave_uniform((int)threadIdx.x >> 6) : (int)threadIdx.x >> 6;
+}
+
 // The wave's own 32-row tile of a [2][NG][32 * D] staging array (an idle buffer at the end of the
 // kernel): every layout holds at least kWaves of them.
 template <int NG, int TE>
@@ -47,9 +63,9 @@ __device__ __forceinline__ uint16_t* wave_tile(uint16_t (&arr)[2][NG][TE], int w
 }
 
 template <int D, class E>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D>(), 8))) void attn_bwd_dq_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(dq_waves<D>(), 8))) void attn_bwd_dq_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
-  constexpr int NG = bwd_group<D>();
+  constexpr int NG = dq_group<D>();
   // Head dims of 64 and more stage K / V blocks by direct global -> LDS loads into dense swizzled
   // tiles (frees the staging VGPRs: -7 % at D = 128, -2 % of the C3 step at D = 64 under the
   // iterative ILP schedule); smaller ones through registers into padded tiles.
@@ -61,7 +77,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
   __shared__ int s_span[4 * kWaves];
 
   const MaskSpec m = a.m;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index<D>();
   const int g = lane >> 5, c32 = lane & 31;
   int b, h;
   TilePlan tp;
@@ -314,7 +330,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
   __shared__ int s_span[2 * kWaves];
 
   const MaskSpec m = a.m;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_index<D>();
   const int g = lane >> 5, c32 = lane & 31;
   int b, h;
   TilePlan tp;
