@@ -338,7 +338,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
   const RowView row = row_view(a, b, tp.mono);
   KState st;
   int run_end;
-  const bool planned = k_begin(a, tp, row, s_span, st, run_end);
+  // (The f16 dK/dV kernel at D = 256 keeps the span reductions: with the four-lane reads the
+  // compiler's AGPR-copy rewrite crashes on it.)
+  constexpr bool kMono = D != 256;
+  const bool planned = k_begin<kMono>(a, tp, row, s_span, st, run_end);
   const int kp = st.kp;
   const bool kvalid = st.kvalid;
   const int nc = st.nc;
@@ -449,7 +452,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
       issue_dma(0, 0);
     else
       issue_regs(0, 0);
-    if (planned) k_lanes(m, run_end, st);
+    if (planned) k_lanes<kMono>(m, run_end, st);
     // The dP tile starts from the -Delta seeds of its query rows, so it comes out of the MFMAs as
     // dP - Delta and dS = P * dP' is one VALU operation per element; the S tile is scaled in fp32 by
     // one FMA per score with the -LSE seeds (S * scale2 - LSE), never by rounding a scaled K.

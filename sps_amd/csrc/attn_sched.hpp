@@ -59,12 +59,12 @@ struct Interval {
 __host__ __device__ __forceinline__ int imin(int x, int y) { return x < y ? x : y; }
 __host__ __device__ __forceinline__ int imax(int x, int y) { return x > y ? x : y; }
 
-__device__ __forceinline__ int stream_parity(const MaskSpec& m, int stream) {
+__host__ __device__ __forceinline__ int stream_parity(const MaskSpec& m, int stream) {
   return stream == STREAM_PERSISTENT ? m.P : 1 - m.P;
 }
 
 // Position of index t of a stream.
-__device__ __forceinline__ int stream_pos(const MaskSpec& m, int stream, int t) {
+__host__ __device__ __forceinline__ int stream_pos(const MaskSpec& m, int stream, int t) {
   return stream == STREAM_NATURAL ? t : 2 * t + stream_parity(m, stream);
 }
 
@@ -77,7 +77,7 @@ __host__ __device__ __forceinline__ int stream_len(int family, int N, int stream
 
 // Keys of stream 0 (natural or persistent) and stream 1 (temporary) visible to query q whose
 // document run starts at position s.
-__device__ __forceinline__ void query_intervals(const MaskSpec& m, int q, int s, Interval& r0, Interval& r1) {
+__host__ __device__ __forceinline__ void query_intervals(const MaskSpec& m, int q, int s, Interval& r0, Interval& r1) {
   if (m.family == FAMILY_FULL) {
     r0.lo = s;
     r0.hi = q;
@@ -107,7 +107,7 @@ __device__ __forceinline__ void query_intervals(const MaskSpec& m, int q, int s,
 
 // Last query position that sees key k (position) of `stream`, whose document run ends at e.
 // The first such query is k itself.
-__device__ __forceinline__ int key_last_query(const MaskSpec& m, int stream, int k, int e) {
+__host__ __device__ __forceinline__ int key_last_query(const MaskSpec& m, int stream, int k, int e) {
   if (m.family == FAMILY_FULL) return e;
   const int tk = k >> 1;
   if (stream == STREAM_PERSISTENT) {
@@ -145,6 +145,25 @@ __device__ __forceinline__ WaveSpan wave_span(const Interval& r) {
   w.max_hi = __builtin_amdgcn_readfirstlane(wave_reduce(empty ? kEmptyHi : r.hi, [](int x, int y) { return imax(x, y); }));
   w.max_lo = __builtin_amdgcn_readfirstlane(wave_reduce(empty ? kEmptyLo : r.lo, [](int x, int y) { return imax(x, y); }));
   w.min_hi = __builtin_amdgcn_readfirstlane(wave_reduce(empty ? kEmptyHi : r.hi, [](int x, int y) { return imin(x, y); }));
+  return w;
+}
+
+// The same spans for intervals that never decrease along the lanes 0-31 (lanes 32-63 repeat them):
+// the union runs from the first non-empty lane's lo to the last non-empty lane's hi, and the common
+// part, when no lane is empty, from lane 31's lo to lane 0's hi; four lane reads instead of four
+// reductions. The kernels' lanes hold consecutive queries (keys) of one stream, and both bounds of
+// their intervals are non-decreasing in the position (run starts and ends, the diagonal and the
+// window bounds all are).
+__device__ __forceinline__ WaveSpan wave_span_monotone(const Interval& r) {
+  const uint64_t ne = __builtin_amdgcn_ballot_w64(r.lo <= r.hi) & 0xffffffffull;
+  if (ne == 0) return WaveSpan{kEmptyLo, kEmptyHi, kEmptyLo, kEmptyHi};
+  const int first = __builtin_ctzll(ne), last = 63 - __builtin_clzll(ne);
+  const bool all = ne == 0xffffffffull;
+  WaveSpan w;
+  w.min_lo = __builtin_amdgcn_readlane(r.lo, first);
+  w.max_hi = __builtin_amdgcn_readlane(r.hi, last);
+  w.max_lo = all ? __builtin_amdgcn_readlane(r.lo, 31) : kEmptyLo;
+  w.min_hi = all ? __builtin_amdgcn_readlane(r.hi, 0) : kEmptyHi;
   return w;
 }
 
@@ -190,7 +209,7 @@ __host__ __device__ __forceinline__ int k_tiles(int family, int N, int P) {
 }
 
 // Stream and first stream index of key tile kt.
-__device__ __forceinline__ void k_tile_run(const MaskSpec& m, int kt, int& stream, int& first) {
+__host__ __device__ __forceinline__ void k_tile_run(const MaskSpec& m, int kt, int& stream, int& first) {
   if (m.family == FAMILY_FULL) {
     stream = STREAM_NATURAL;
     first = kt * kTile;

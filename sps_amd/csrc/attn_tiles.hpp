@@ -226,8 +226,8 @@ __device__ __forceinline__ void q_lanes(const MaskSpec& m, int qp, int s, QState
     st.r0 = Interval{kEmptyLo, kEmptyHi};
     st.r1 = st.r0;
   }
-  st.w0 = wave_span(st.r0);
-  st.w1 = wave_span(st.r1);
+  st.w0 = wave_span_monotone(st.r0);
+  st.w1 = wave_span_monotone(st.r1);
 }
 
 // The workgroup's key-block plan: per stream, the 32-row blocks covering the union of its lanes'
@@ -326,6 +326,8 @@ __device__ __forceinline__ void k_lane_key(const MaskSpec& m, int kt, KState& st
 }
 
 // The lane's query interval and the wave span, given the end e of the key's document run.
+// kMonotone: the span from four lane reads (wave_span_monotone), else from four reductions.
+template <bool kMonotone = true>
 __device__ __forceinline__ void k_lanes(const MaskSpec& m, int e, KState& st) {
   if (st.kvalid) {
     st.r.lo = st.kp;
@@ -334,7 +336,7 @@ __device__ __forceinline__ void k_lanes(const MaskSpec& m, int e, KState& st) {
   } else {
     st.r = Interval{kEmptyLo, kEmptyHi};
   }
-  st.w = wave_span(st.r);
+  st.w = kMonotone ? wave_span_monotone(st.r) : wave_span(st.r);
 }
 
 // Query chunks covering the union of the workgroup's lane intervals (one LDS exchange and barrier).
@@ -356,19 +358,21 @@ __device__ __forceinline__ void k_plan_from_spans(int* s_span, KState& st) {
   st.nc = wave_uniform(st.nc);
 }
 
+template <bool kMonotone = true>
 __device__ __forceinline__ void k_setup(const AttnArgs& a, const RowView& row, int kt, int* s_span, KState& st) {
   k_lane_key(a.m, kt, st);
-  k_lanes(a.m, st.kvalid ? row.run_end(st.kp, a.m.N) : 0, st);
+  k_lanes<kMonotone>(a.m, st.kvalid ? row.run_end(st.kp, a.m.N) : 0, st);
   k_plan_from_spans(s_span, st);
 }
 
 // Start of a key-stationary workgroup; as q_begin, with the lane's run end read here and consumed by
 // k_lanes(m, run_end, st) after the caller's first loads are issued.
+template <bool kMonotone = true>
 __device__ __forceinline__ bool k_begin(const AttnArgs& a, const TilePlan& tp, const RowView& row, int* s_span,
                                         KState& st, int& run_end) {
   run_end = 0;
   if (tp.n0 < 0) {
-    k_setup(a, row, tp.tile, s_span, st);
+    k_setup<kMonotone>(a, row, tp.tile, s_span, st);
     return false;
   }
   k_lane_key(a.m, tp.tile, st);

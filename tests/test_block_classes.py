@@ -21,3 +21,17 @@ def test_closed_form_block_classes(tmp_path):
     out = subprocess.run([str(exe), "200000"], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stdout + out.stderr
     assert out.stdout.strip().endswith("bad 0")
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(),
+                    reason="hipcc not available")
+def test_lane_intervals_are_monotone(tmp_path):
+    # The kernels read a wave's span from four lanes (wave_span_monotone); this holds only while the
+    # lanes' intervals never decrease along the lanes, which the host check verifies by brute force.
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    exe = tmp_path / "lane_spans_check"
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-O2", "-std=c++17", "-w",
+                    str(HERE / "native" / "lane_spans_check.hip"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe), "400"], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert out.stdout.strip().endswith("bad 0")
