@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(dq_waves<D>
   // tiles (frees the staging VGPRs: -7 % at D = 128, -2 % of the C3 step at D = 64 under the
   // iterative ILP schedule); smaller ones through registers into padded tiles.
   constexpr bool kDma = D >= 64;
-  using DT = DmaTile<kDma ? D : 64>;
+  using DT = DmaTile<kDma ? D : 64, (D != 64)>;  // D = 64: the register-lean swizzle (3 waves per SIMD)
   constexpr int TE = kDma ? DT::ELEMS : G::ELEMS;
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][NG][TE];  // [buffer][block of the group]
   __shared__ __attribute__((aligned(16))) uint16_t sV[2][NG][TE];

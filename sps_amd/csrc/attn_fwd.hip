@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
   // tiles (no staging registers, no LDS write instructions); smaller ones through registers into
   // padded tiles.
   constexpr bool kDma = D >= 64;
-  using DT = DmaTile<kDma ? D : 64>;
+  using DT = DmaTile<kDma ? D : 64, false>;
   constexpr int TE = kDma ? DT::ELEMS : G::ELEMS;
   // One array per buffer ([block of the pair]): every use names its buffer with a compile-time
   // index, so the compiler can tell the buffers apart, and the score-tile reads of one buffer do not

@@ -85,18 +85,33 @@ struct TileRegs {
 };
 
 // Dense LDS tile filled by direct global -> LDS loads (head dims of 64 and more): 32 rows of D
-// elements, no padding. The 16-byte chunk c of row r is stored at chunk c ^ swz(r), with
-// swz(r) = 2 (r % 4) + (r / 4) % 2: the 8 consecutive rows that a fragment load reads in one chunk
-// land in 8 distinct chunk slots, and the 4 rows x 2 chunks of each 16-lane group of a transposed
-// read in 4 distinct chunk pairs, so neither access pattern needs the padding column.
-template <int D>
+// elements, no padding; the 16-byte chunks of each row are permuted by a row-dependent swizzle
+// instead (swz below).
+template <int D, bool kSpread = true>
 struct DmaTile {
-  static_assert(D % 64 == 0, "the swizzle needs at least 8 chunks per row");
+  static_assert(D == 64 || D % 128 == 0, "the swizzle permutes 8 chunks of a row at D = 64, 16 above");
   static constexpr int CPR = D / 8;                  // 16-byte chunks per row
   static constexpr int ELEMS = kBlock * D;           // one staged tile
   static constexpr int PASSES = ELEMS / (256 * 8);   // 16-byte pieces per thread (1 for D = 64)
 
-  static __device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+  // Logical chunk k of row r is stored at chunk k ^ swz(r), so that both fragment reads below hit
+  // distinct LDS banks (64 banks of 4 bytes): a row-fragment b128 read gives 16 lanes 16 consecutive
+  // rows at one logical chunk, a transposed b64 read gives 32 lanes rows r0 .. r0 + 3 at four
+  // consecutive chunks. D = 64 (a row covers half the banks): the rows of one parity among 16
+  // consecutive rows get 8 different swizzles (bits 1-3 of r), and rows r, r + 2 different 4-chunk
+  // groups (swizzle bit 2 = bit 1 of r). D >= 128 (a row covers every bank): 16 consecutive rows get
+  // 16 different swizzles, and rows r0 .. r0 + 3 different 4-chunk groups (swizzle bits 2-3 = r & 3).
+  // kSpread false keeps an older 3-bit swizzle under which rows r and r + 8 share a swizzle (so a
+  // transposed fragment needs one address per lane instead of two; row-fragment reads then meet
+  // 2-way bank conflicts), for kernels whose registers are the tighter limit.
+  static __device__ __forceinline__ int swz(int r) {
+    if constexpr (!kSpread)
+      return ((r & 3) << 1) | ((r >> 2) & 1);
+    else if constexpr (D == 64)
+      return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
+    else
+      return ((r & 3) << 2) | ((r >> 2) & 3);
+  }
 
   // Byte offsets, from the tile's first row, of the pieces thread tid loads: piece p fills slot
   // p * 256 + tid of the tile (row slot / CPR, stored chunk slot % CPR).
@@ -121,16 +136,16 @@ struct DmaTile {
   }
 
   // Element offset of row c32's chunk 2c + g (row-major fragment: 8 consecutive columns 16c + 8g).
-  static __device__ __forceinline__ int frag(int c32, int g, int c) { return c32 * D + ((2 * c) ^ (g ^ swz(c32))) * 8; }
+  static __device__ __forceinline__ int frag(int c32, int g, int c) { return c32 * D + ((2 * c + g) ^ swz(c32)) * 8; }
 
-  // The transposed fragment of lds_frag_tr(tile, row_stride, r0, 32 dc, lane) on this layout
-  // (r0 a multiple of 8, so rows r and r + 8 share a swizzle).
+  // The transposed fragment of lds_frag_tr(tile, row_stride, r0, 32 dc, lane) on this layout.
   static __device__ __forceinline__ u32x4_t frag_tr(const uint16_t* tile, int r0, int dc, int lane) {
     const int s = lane & 15, grp = lane >> 4;
     const int row = r0 + 4 * (grp >> 1) + (s >> 2);
-    const int y = (2 * (grp & 1) + ((s & 3) >> 1)) ^ swz(row);
-    const uint16_t* p = tile + row * D + ((4 * dc) ^ y) * 8 + 4 * (s & 1);
-    const u32x2_t lo = lds_read_tr16(p), hi = lds_read_tr16(p + 8 * D);
+    const int k = 4 * dc + 2 * (grp & 1) + ((s & 3) >> 1);  // logical chunk
+    const uint16_t* p = tile + row * D + (k ^ swz(row)) * 8 + 4 * (s & 1);
+    const uint16_t* q = kSpread ? tile + (row + 8) * D + (k ^ swz(row + 8)) * 8 + 4 * (s & 1) : p + 8 * D;
+    const u32x2_t lo = lds_read_tr16(p), hi = lds_read_tr16(q);
     return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
   }
 };
