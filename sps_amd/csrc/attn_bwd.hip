@@ -70,7 +70,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(dq_waves<D>
   // tiles (frees the staging VGPRs: -7 % at D = 128, -2 % of the C3 step at D = 64 under the
   // iterative ILP schedule); smaller ones through registers into padded tiles.
   constexpr bool kDma = D >= 64;
-  using DT = DmaTile<kDma ? D : 64, (D != 64)>;  // D = 64: the register-lean swizzle (3 waves per SIMD)
+  // The conflict-free swizzle costs a few address VGPRs: at D = 64 (3 waves per SIMD) and D = 256
+  // they would spill, so those keep the register-lean one.
+  using DT = DmaTile<kDma ? D : 64, D == 128>;
   constexpr int TE = kDma ? DT::ELEMS : G::ELEMS;
   __shared__ __attribute__((aligned(16))) uint16_t sK[2][NG][TE];  // [buffer][block of the group]
   __shared__ __attribute__((aligned(16))) uint16_t sV[2][NG][TE];
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
   // Head dims of 64 and more stage Q / dO chunks and their seeds by direct global -> LDS loads into
   // dense swizzled tiles; smaller ones through registers into padded tiles.
   constexpr bool kDma = D >= 64;
-  using DT = DmaTile<kDma ? D : 64>;
+  using DT = DmaTile<kDma ? D : 64, D != 256>;  // D = 256: the register-lean swizzle (fewer spills)
   constexpr int TE = kDma ? DT::ELEMS : G::ELEMS;
   __shared__ __attribute__((aligned(16))) uint16_t sQ[2][NG][TE];  // [buffer][chunk of the group]
   __shared__ __attribute__((aligned(16))) uint16_t sDO[2][NG][TE];

@@ -136,15 +136,27 @@ struct DmaTile {
   }
 
   // Element offset of row c32's chunk 2c + g (row-major fragment: 8 consecutive columns 16c + 8g).
-  static __device__ __forceinline__ int frag(int c32, int g, int c) { return c32 * D + ((2 * c + g) ^ swz(c32)) * 8; }
+  static __device__ __forceinline__ int frag(int c32, int g, int c) {
+    if constexpr (kSpread)
+      return c32 * D + ((2 * c + g) ^ swz(c32)) * 8;
+    else
+      return c32 * D + ((2 * c) ^ (g ^ swz(c32))) * 8;
+  }
 
-  // The transposed fragment of lds_frag_tr(tile, row_stride, r0, 32 dc, lane) on this layout.
+  // The transposed fragment of lds_frag_tr(tile, row_stride, r0, 32 dc, lane) on this layout
+  // (r0 a multiple of 8; rows r and r + 8 share a swizzle only when !kSpread).
   static __device__ __forceinline__ u32x4_t frag_tr(const uint16_t* tile, int r0, int dc, int lane) {
     const int s = lane & 15, grp = lane >> 4;
     const int row = r0 + 4 * (grp >> 1) + (s >> 2);
-    const int k = 4 * dc + 2 * (grp & 1) + ((s & 3) >> 1);  // logical chunk
-    const uint16_t* p = tile + row * D + (k ^ swz(row)) * 8 + 4 * (s & 1);
-    const uint16_t* q = kSpread ? tile + (row + 8) * D + (k ^ swz(row + 8)) * 8 + 4 * (s & 1) : p + 8 * D;
+    const int t = 2 * (grp & 1) + ((s & 3) >> 1);  // logical chunk 4 dc + t
+    const uint16_t *p, *q;
+    if constexpr (kSpread) {
+      p = tile + row * D + ((4 * dc + t) ^ swz(row)) * 8 + 4 * (s & 1);
+      q = tile + (row + 8) * D + ((4 * dc + t) ^ swz(row + 8)) * 8 + 4 * (s & 1);
+    } else {
+      p = tile + row * D + ((4 * dc) ^ (t ^ swz(row))) * 8 + 4 * (s & 1);
+      q = p + 8 * D;
+    }
     const u32x2_t lo = lds_read_tr16(p), hi = lds_read_tr16(q);
     return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
   }
