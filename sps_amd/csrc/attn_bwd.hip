@@ -461,65 +461,77 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
     const float scale2 = a.scale2;
     auto cls_of = [&](int i) { return classify_block(st.w, (st.c0 + i) * kBlock, EXACT); };
     const BlockMask bm = k_block_mask(st, EXACT);
+    // S and dP tiles of block y of the group (the dP tile starts from its rows' -Delta seeds).
+    auto sdp = [&](int y, int buf, f32x16_t& sc, f32x16_t& dp) {
+      const uint16_t* tQ = sQ[buf][y];
+      const uint16_t* tDO = sDO[buf][y];
+      sc = f32x16_t{};
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        // Query rows 8*i4 + 4g + {0..3} of this chunk.
+        const f32x4_t d4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
+            (const SPS_LDS float*)(&sSeed[buf][y][kBlock + 8 * i4 + 4 * g]));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) dp[4 * i4 + t] = d4[t];
+      }
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        sc = E::mfma(row_frag(tQ, c), kf[c], sc);
+        dp = E::mfma(row_frag(tDO, c), vf[c], dp);
+      }
+    };
+    // Block y's S tile in fp32 (S * scale2 - LSE, the -LSE seeds read here), masked when partial.
+    auto scores = [&](int y, int buf, int qc, bool full, f32x16_t& sc) {
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f32x4_t l4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
+            (const SPS_LDS float*)(&sSeed[buf][y][8 * i4 + 4 * g]));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) sc[4 * i4 + t] = __builtin_fmaf(sc[4 * i4 + t], scale2, l4[t]);
+      }
+      if (!full)
+        mask_partial<EXACT>(sc, st.r, st.w, qc, g, [&] { return ks_exact_bits(a, b, kp, st.r.hi, qc, g, dk_doc); });
+    };
+    // P and dS of block y, then the dV and dK products.
+    auto grads = [&](int y, int buf, const f32x16_t& sc, const f32x16_t& dp) {
+      const uint16_t* tQ = sQ[buf][y];
+      const uint16_t* tDO = sDO[buf][y];
+      uint32_t pk[8], dsk[8];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        float p[4], ds[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int e = 4 * i4 + t;
+          p[t] = fast_exp2(sc[e]);
+          ds[t] = p[t] * dp[e];
+        }
+        pk[2 * i4] = E::pack2(p[0], p[1]);
+        pk[2 * i4 + 1] = E::pack2(p[2], p[3]);
+        dsk[2 * i4] = E::pack2(ds[0], ds[1]);
+        dsk[2 * i4 + 1] = E::pack2(ds[2], ds[3]);
+      }
+#pragma unroll
+      for (int dc = 0; dc < G::DC; ++dc) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const u32x4_t pf = {pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]};
+          const u32x4_t df = {dsk[4 * kh], dsk[4 * kh + 1], dsk[4 * kh + 2], dsk[4 * kh + 3]};
+          dv[dc] = E::mfma(tr_frag(tDO, kh, dc), pf, dv[dc]);
+          dk[dc] = E::mfma(tr_frag(tQ, kh, dc), df, dk[dc]);
+        }
+      }
+    };
     auto body = [&](int j, int buf) {
       int act2, full2;
       group_codes<NG>(bm, NG * j, nc, cls_of, act2, full2);
 #pragma unroll
       for (int y = 0; y < NG; ++y) {
-        const int i = NG * j + y;
-        const int qc = (st.c0 + i) * kBlock;
         if ((act2 >> y) & 1) {
-          const uint16_t* tQ = sQ[buf][y];
-          const uint16_t* tDO = sDO[buf][y];
-          f32x16_t sc = f32x16_t{}, dp, nl;
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) {
-            // Query rows 8*i4 + 4g + {0..3} of this chunk.
-            const f32x4_t l4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                (const SPS_LDS float*)(&sSeed[buf][y][8 * i4 + 4 * g]));
-            const f32x4_t d4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-                (const SPS_LDS float*)(&sSeed[buf][y][kBlock + 8 * i4 + 4 * g]));
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              nl[4 * i4 + t] = l4[t];
-              dp[4 * i4 + t] = d4[t];
-            }
-          }
-#pragma unroll
-          for (int c = 0; c < D / 16; ++c) {
-            sc = E::mfma(row_frag(tQ, c), kf[c], sc);
-            dp = E::mfma(row_frag(tDO, c), vf[c], dp);
-          }
-#pragma unroll
-          for (int e = 0; e < 16; ++e) sc[e] = __builtin_fmaf(sc[e], scale2, nl[e]);
-          if (!((full2 >> y) & 1))
-            mask_partial<EXACT>(sc, st.r, st.w, qc, g,
-                                [&] { return ks_exact_bits(a, b, kp, st.r.hi, qc, g, dk_doc); });
-          uint32_t pk[8], dsk[8];
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) {
-            float p[4], ds[4];
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              const int e = 4 * i4 + t;
-              p[t] = fast_exp2(sc[e]);
-              ds[t] = p[t] * dp[e];
-            }
-            pk[2 * i4] = E::pack2(p[0], p[1]);
-            pk[2 * i4 + 1] = E::pack2(p[2], p[3]);
-            dsk[2 * i4] = E::pack2(ds[0], ds[1]);
-            dsk[2 * i4 + 1] = E::pack2(ds[2], ds[3]);
-          }
-#pragma unroll
-          for (int dc = 0; dc < G::DC; ++dc) {
-#pragma unroll
-            for (int kh = 0; kh < 2; ++kh) {
-              const u32x4_t pf = {pk[4 * kh], pk[4 * kh + 1], pk[4 * kh + 2], pk[4 * kh + 3]};
-              const u32x4_t df = {dsk[4 * kh], dsk[4 * kh + 1], dsk[4 * kh + 2], dsk[4 * kh + 3]};
-              dv[dc] = E::mfma(tr_frag(tDO, kh, dc), pf, dv[dc]);
-              dk[dc] = E::mfma(tr_frag(tQ, kh, dc), df, dk[dc]);
-            }
-          }
+          f32x16_t sc, dp;
+          sdp(y, buf, sc, dp);
+          scores(y, buf, (st.c0 + NG * j + y) * kBlock, (full2 >> y) & 1, sc);
+          grads(y, buf, sc, dp);
         }
       }
     };
