@@ -28,6 +28,14 @@ __host__ __device__ __forceinline__ void cover_blocks(int lo, int hi, int& first
   count = hi >= lo ? hi / kBlock - first + 1 : 0;
 }
 
+// Workgroup barrier ordering LDS accesses only (fences limited to the local address space):
+// global stores issued before it keep draining, where __syncthreads() would wait for them.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 struct AttnArgs {
   const uint16_t* q;
   const uint16_t* k;

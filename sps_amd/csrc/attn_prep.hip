@@ -8,7 +8,7 @@
 //
 // It also writes the work plan of every query tile and key tile (the 32-row blocks covering the
 // union of the tile's lanes' visible intervals, per stream: exactly what the kernels would derive
-// from the run bounds) in decreasing order of block count, so the heaviest workgroups are
+// from the run bounds, in closed form from the tile's first and last rows) in decreasing order of block count, so the heaviest workgroups are
 // dispatched first and each workgroup starts its first tile loads after reading one plan. The order
 // only affects speed: it is always a permutation of the tiles.
 #include "attn_kernels.hpp"
@@ -29,63 +29,6 @@ struct RunBounds {
   __device__ __forceinline__ int start(int p) const { return s_lds ? s_lds[p] : s_glb[p]; }
   __device__ __forceinline__ int end(int p) const { return e_lds ? e_lds[p] : e_glb[p]; }
 };
-
-// Tile plans are computed by rows of 16 lanes (one DPP row per tile, every tile of the row at once):
-// each lane folds 8 of the tile's 128 positions, then the row reduces with four DPP moves, after
-// which every lane of the row holds the result.
-constexpr int kPlanLanes = 16;
-
-template <class Op>
-__device__ __forceinline__ int row16_reduce(int x, Op op) {
-  x = op(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));   // quad_perm [1, 0, 3, 2]
-  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));   // quad_perm [2, 3, 0, 1]
-  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false));  // row_half_mirror
-  return op(x, __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false));  // row_mirror
-}
-__device__ __forceinline__ int row_min(int x) { return row16_reduce(x, [](int u, int v) { return imin(u, v); }); }
-__device__ __forceinline__ int row_max(int x) { return row16_reduce(x, [](int u, int v) { return imax(u, v); }); }
-
-// Plan of query tile qt, computed by one 16-lane row (lane l takes queries qa + l, qa + l + 16, ..):
-// per stream, the blocks covering the union of the queries' key intervals, as q_setup derives it.
-__device__ void q_tile_plan(const MaskSpec& m, const RunBounds& rb, int qt, int& b0, int& n0, int& b1, int& n1) {
-  int lo0 = kEmptyLo, hi0 = kEmptyHi, lo1 = kEmptyLo, hi1 = kEmptyHi;
-#pragma unroll
-  for (int k = 0; k < kTile / kPlanLanes; ++k) {  // unrolled: the run-bound reads go out together
-    const int q = qt * kTile + threadIdx.x % kPlanLanes + kPlanLanes * k;
-    if (q < m.N) {
-      Interval i0, i1;
-      query_intervals(m, q, rb.start(q), i0, i1);  // an empty interval is {kEmptyLo, kEmptyHi}
-      lo0 = imin(lo0, i0.lo);
-      hi0 = imax(hi0, i0.hi);
-      lo1 = imin(lo1, i1.lo);
-      hi1 = imax(hi1, i1.hi);
-    }
-  }
-  cover_blocks(row_min(lo0), row_max(hi0), b0, n0);
-  cover_blocks(row_min(lo1), row_max(hi1), b1, n1);
-}
-
-// Plan of key tile kt, computed by one 16-lane row: the query chunks covering the union of its
-// keys' query intervals [k, last query seeing k], as k_setup derives it.
-__device__ void k_tile_plan(const MaskSpec& m, const RunBounds& rb, int kt, int& c0, int& nc) {
-  int stream, first;
-  k_tile_run(m, kt, stream, first);
-  const int len = stream_len(m.family, m.N, stream, m.P);
-  int lo = kEmptyLo, hi = kEmptyHi;
-#pragma unroll
-  for (int k = 0; k < kTile / kPlanLanes; ++k) {
-    const int t = first + threadIdx.x % kPlanLanes + kPlanLanes * k;
-    if (t < len) {
-      const int kp = stream_pos(m, stream, t);
-      const int last = key_last_query(m, stream, kp, rb.end(kp));
-      if (last >= kp) {
-        lo = imin(lo, kp);
-        hi = imax(hi, last);
-      }
-    }
-  }
-  cover_blocks(row_min(lo), row_max(hi), c0, nc);
-}
 
 // Exclusive scans of the per-thread chunk summaries, both in one pass so their latencies overlap:
 // a max-scan of `up` in thread order and a min-scan of `down` in reverse thread order. Inside each
@@ -265,65 +208,10 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   }
   if (tid == 0) a.row_mono[b] = mono ? 1 : 0;
   __syncthreads();  // start/end of the whole row are visible to every thread below
-  // Rows that fit read their run bounds from LDS (short: positions < kLdsRow <= 32767).
-  const bool lds_ok = in_regs;
-  const RunBounds rb = {lds_ok ? s_start : nullptr, lds_ok ? s_end : nullptr, start, end};
-
-  // Query-tile and key-tile plans (one wave per tile), then both sorts. Rows with more than
-  // kMaxSortTiles tiles keep the closed-form order (query tiles last to first, key tiles first to
-  // last) and write their plans directly.
-  const int nqt = q_tiles(N);
-  const int nkt = k_tiles(m.family, N, m.P);
-  const bool sort_q = nqt <= kMaxSortTiles, sort_k = nkt <= kMaxSortTiles;
-  TilePlan* qplan = a.q_plan + (int64_t)b * nqt;
-  TilePlan* kplan = a.k_plan + (int64_t)b * nkt;
-  const int mono_flag = mono ? 1 : 0;
-  const bool lead = tid % kPlanLanes == 0;
-  constexpr int kRows = kPrepThreads / kPlanLanes;
-  // Query tiles are units [0, nqt), key tiles units [nqt, nqt + nkt); row tid / 16 takes every
-  // kRows-th unit.
-  for (int u = tid / kPlanLanes; u < nqt + nkt; u += kRows) {
-    if (u < nqt) {
-      const int t = u;
-      int b0, n0, b1, n1;
-      q_tile_plan(m, rb, t, b0, n0, b1, n1);
-      if (!lead) continue;
-      if (sort_q) {
-        s_cost[t] = n0 + n1;
-        s_qplan[t][0] = b0;
-        s_qplan[t][1] = n0;
-        s_qplan[t][2] = b1;
-        s_qplan[t][3] = n1;
-      } else {
-        qplan[nqt - 1 - t] = TilePlan{t, mono_flag, b0, n0, b1, n1, 0, 0};
-      }
-    } else {
-      const int t = u - nqt;
-      int c0, nc;
-      k_tile_plan(m, rb, t, c0, nc);
-      if (!lead) continue;
-      if (sort_k) {
-        s_cost_k[t] = nc;
-        s_kplan[t][0] = c0;
-        s_kplan[t][1] = nc;
-      } else {
-        kplan[t] = TilePlan{t, mono_flag, c0, nc, 0, 0, 0, 0};
-      }
-    }
-  }
-  __syncthreads();
-  if (sort_q)
-    sort_tiles(s_cost, nqt, 0, kPrepThreads / 2, [&](int r, int t) {
-      qplan[r] = TilePlan{t, mono_flag, s_qplan[t][0], s_qplan[t][1], s_qplan[t][2], s_qplan[t][3], 0, 0};
-    });
-  if (sort_k)
-    sort_tiles(s_cost_k, nkt, kPrepThreads / 2, kPrepThreads / 2, [&](int r, int t) {
-      kplan[r] = TilePlan{t, mono_flag, s_kplan[t][0], s_kplan[t][1], 0, 0, 0, 0};
-    });
   if (in_regs) {
-    // Rows held in LDS reach global memory last, so no barrier above waits for these stores: one
-    // pass of consecutive positions per thread group, 4 per thread (16-byte stores) when the row
-    // length allows.
+    // Rows held in LDS go to global memory now: one pass of consecutive positions per thread group,
+    // 4 per thread (16-byte stores) when the row length allows; the stores drain while the plans
+    // below are computed (the barrier before the sorts is the first to wait for them).
     if ((N & 3) == 0) {
       for (int p = 4 * tid; p < N; p += 4 * kPrepThreads) {
         *reinterpret_cast<int4*>(start + p) = make_int4(s_start[p], s_start[p + 1], s_start[p + 2], s_start[p + 3]);
@@ -336,6 +224,63 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
       }
     }
   }
+  // Rows that fit read their run bounds from LDS (short: positions < kLdsRow <= 32767).
+  const bool lds_ok = in_regs;
+  const RunBounds rb = {lds_ok ? s_start : nullptr, lds_ok ? s_end : nullptr, start, end};
+
+  // Query-tile and key-tile plans, then both sorts. Rows with more than
+  // kMaxSortTiles tiles keep the closed-form order (query tiles last to first, key tiles first to
+  // last) and write their plans directly.
+  const int nqt = q_tiles(N);
+  const int nkt = k_tiles(m.family, N, m.P);
+  const bool sort_q = nqt <= kMaxSortTiles, sort_k = nkt <= kMaxSortTiles;
+  TilePlan* qplan = a.q_plan + (int64_t)b * nqt;
+  TilePlan* kplan = a.k_plan + (int64_t)b * nkt;
+  const int mono_flag = mono ? 1 : 0;
+  auto st_of = [&](int q) { return rb.start(q); };
+  auto en_of = [&](int k) { return rb.end(k); };
+  // Query tiles are units [0, nqt), key tiles units [nqt, nqt + nkt); one thread per unit, each plan
+  // from the tile's first and last few rows (q_tile_union / k_tile_union).
+  for (int u = tid; u < nqt + nkt; u += kPrepThreads) {
+    if (u < nqt) {
+      const int t = u;
+      Interval u0, u1;
+      q_tile_union(m, t, st_of, u0, u1);
+      int b0, n0, b1, n1;
+      cover_blocks(u0.lo, u0.hi, b0, n0);
+      cover_blocks(u1.lo, u1.hi, b1, n1);
+      if (sort_q) {
+        s_cost[t] = n0 + n1;
+        s_qplan[t][0] = b0;
+        s_qplan[t][1] = n0;
+        s_qplan[t][2] = b1;
+        s_qplan[t][3] = n1;
+      } else {
+        qplan[nqt - 1 - t] = TilePlan{t, mono_flag, b0, n0, b1, n1, 0, 0};
+      }
+    } else {
+      const int t = u - nqt;
+      const Interval k = k_tile_union(m, t, en_of);
+      int c0, nc;
+      cover_blocks(k.lo, k.hi, c0, nc);
+      if (sort_k) {
+        s_cost_k[t] = nc;
+        s_kplan[t][0] = c0;
+        s_kplan[t][1] = nc;
+      } else {
+        kplan[t] = TilePlan{t, mono_flag, c0, nc, 0, 0, 0, 0};
+      }
+    }
+  }
+  lds_barrier();  // the plans and costs are in LDS; the run-bound stores above keep draining
+  if (sort_q)
+    sort_tiles(s_cost, nqt, 0, kPrepThreads / 2, [&](int r, int t) {
+      qplan[r] = TilePlan{t, mono_flag, s_qplan[t][0], s_qplan[t][1], s_qplan[t][2], s_qplan[t][3], 0, 0};
+    });
+  if (sort_k)
+    sort_tiles(s_cost_k, nkt, kPrepThreads / 2, kPrepThreads / 2, [&](int r, int t) {
+      kplan[r] = TilePlan{t, mono_flag, s_kplan[t][0], s_kplan[t][1], 0, 0, 0, 0};
+    });
 }
 
 hipError_t launch_row_layout(const AttnArgs& a, hipStream_t stream) {

@@ -117,6 +117,37 @@ __host__ __device__ __forceinline__ int key_last_query(const MaskSpec& m, int st
   return imin(e, 2 * (tk + m.window) + 1);
 }
 
+// Union, per stream, of the intervals of query tile qt's queries (kTile consecutive positions),
+// from its first and last kTileEnds queries only: both interval bounds never decrease with the
+// position (run starts, the diagonal and the window bounds all are non-decreasing), so the union
+// runs from the first non-empty query's lo to the last non-empty query's hi, and among any two
+// consecutive positions at least one has a non-empty interval of a stream unless no position of
+// the tile does (tests/native/tile_plan_check.hip compares this with the union over every query).
+// start(q) is q's run start.
+constexpr int kTileEnds = 4;
+template <class StartFn>
+__host__ __device__ __forceinline__ void q_tile_union(const MaskSpec& m, int qt, StartFn start, Interval& u0,
+                                                      Interval& u1) {
+  u0 = u1 = Interval{kEmptyLo, kEmptyHi};
+  const int qa = qt * kTile, qz = imin(qa + kTile, m.N) - 1;
+  for (int j = 0; j < 2 * kTileEnds; ++j) {
+    const int q = j < kTileEnds ? qa + j : qz - (j - kTileEnds);
+    if (q < qa || q > qz) continue;
+    Interval i0, i1;
+    query_intervals(m, q, start(q), i0, i1);  // an empty interval is {kEmptyLo, kEmptyHi}
+    u0.lo = imin(u0.lo, i0.lo);
+    u0.hi = imax(u0.hi, i0.hi);
+    u1.lo = imin(u1.lo, i1.lo);
+    u1.hi = imax(u1.hi, i1.hi);
+  }
+}
+
+// Union of the query intervals [k, key_last_query(k)] of key tile kt's keys: every key of a stream
+// has a non-empty interval or none has, and the last query never decreases with the key, so the
+// tile's first and last keys give it. end(k) is the end of k's run.
+template <class EndFn>
+__host__ __device__ __forceinline__ Interval k_tile_union(const MaskSpec& m, int kt, EndFn end);
+
 // Per-wave summary of the lanes' intervals: union bounds (for SKIP) and intersection bounds (FULL).
 struct WaveSpan {
   int min_lo, max_hi;  // union [min_lo, max_hi] over lanes with a non-empty interval
@@ -218,6 +249,27 @@ __host__ __device__ __forceinline__ void k_tile_run(const MaskSpec& m, int kt, i
   const int np = k_tiles_stream(m.family, m.N, STREAM_PERSISTENT, m.P);
   stream = kt < np ? STREAM_PERSISTENT : STREAM_TEMPORARY;
   first = (kt < np ? kt : kt - np) * kTile;
+}
+
+// (Definition of k_tile_union, declared above.)
+template <class EndFn>
+__host__ __device__ __forceinline__ Interval k_tile_union(const MaskSpec& m, int kt, EndFn end) {
+  int stream, first;
+  k_tile_run(m, kt, stream, first);
+  const int len = stream_len(m.family, m.N, stream, m.P);
+  const int ta = first, tz = imin(first + kTile, len) - 1;
+  Interval u{kEmptyLo, kEmptyHi};
+  for (int j = 0; j < 2 * kTileEnds; ++j) {
+    const int t = j < kTileEnds ? ta + j : tz - (j - kTileEnds);
+    if (t < ta || t > tz) continue;
+    const int kp = stream_pos(m, stream, t);
+    const int last = key_last_query(m, stream, kp, end(kp));
+    if (last >= kp) {
+      u.lo = imin(u.lo, kp);
+      u.hi = imax(u.hi, last);
+    }
+  }
+  return u;
 }
 
 }  // namespace sps

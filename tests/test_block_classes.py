@@ -35,3 +35,17 @@ def test_lane_intervals_are_monotone(tmp_path):
     out = subprocess.run([str(exe), "400"], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stdout + out.stderr
     assert out.stdout.strip().endswith("bad 0")
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(),
+                    reason="hipcc not available")
+def test_closed_form_tile_plans(tmp_path):
+    # The row-layout prepass derives each tile's plan from the tile's first and last few rows
+    # (q_tile_union / k_tile_union); the host check compares that with the union over every row.
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    exe = tmp_path / "tile_plan_check"
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-O2", "-std=c++17", "-w",
+                    str(HERE / "native" / "tile_plan_check.hip"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe), "20000"], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert out.stdout.strip().endswith("bad 0")
