@@ -132,6 +132,10 @@ MASK_CASES = [
     ("full", 333, 0, "packed", None),
     ("full", 256, 0, "random", None),
     ("sps", 1024, 4096, "packed", None),
+    # closed-form tile plans where every other position sees nothing of a stream (window 0 or -1,
+    # a persistent-key window of 0 or the diagonal only), over documents in runs
+    ("sps", 514, 0, "packed", -1),
+    ("reverse_sps", 386, -1, "packed", 0),
     # rows longer than 8192 positions take the prepass's looped (not register-resident) path
     ("sps", 8320, 64, "packed", None),
     ("full", 8200, 0, "random", None),
