@@ -6,8 +6,10 @@ D 64, 4096 interleaved positions, rows packed with log-normal documents — in u
 (14 * D * visible pairs per step: 4 * D forward, 10 * D backward, the reference's 2.5x convention of
 original_flash_attn.py:749-755). A step is one forward and one backward over the whole batch, with
 inputs resident in HBM. Also reported: C5 segmented decode (µs/step, GB/s), the roofline of the
-dominant kernel of each (timed live with HIP events on the launch stream), and the reference's CPU
-path timed on this host on a bounded sample of the same workload.
+dominant kernel of each (timed live with HIP events on the launch stream), the reference's CPU
+path timed on this host on a bounded sample of the same workload, the C1, C2 and C4 lines, and, for
+context, dense causal attention at C3's shape through this library and through PyTorch's own
+scaled_dot_product_attention.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps S] [--no-cpu-baseline]
 Prints one JSON line on stdout (progress goes to stderr).
@@ -365,6 +367,57 @@ def cpu_attention_baseline(cfg, budget_s: float):
 # ----------------------------------------------------------------------------------------------
 # C1: SPS forward at the reference's CPU-runnable size
 # ----------------------------------------------------------------------------------------------
+def bench_dense_causal(steps: int, warmup: int, b: int = 4, h: int = 16, n: int = 4096, d: int = 64):
+    """Context for the roofline fractions: dense causal attention (no documents, no window) at C3's
+    batch, heads, length and head dim, bf16 fwd+bwd and fwd alone, through this library's
+    full_attention and through PyTorch's own scaled_dot_product_attention (is_causal, each of its
+    fused backends that runs here). Useful FLOPs: 4 D per visible pair forward, 14 D fwd+bwd."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from sps_amd import attention as SA
+
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q, k, v, do = (torch.randn(b, h, n, d, generator=g).to("cuda", torch.bfloat16) for _ in range(4))
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    pairs = b * h * n * (n + 1) // 2
+    scale = 1.0 / math.sqrt(d)
+
+    def measure(fwd):
+        def step():
+            fwd().backward(do)
+
+        out = {}
+        for name, fn in (("fwd_bwd", step), ("fwd", fwd)):
+            settle(fn, SETTLE_MS / 2)
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / steps
+            flops = (14 if name == "fwd_bwd" else 4) * d * pairs
+            out[name] = {"us": round(us, 1), "tflops": round(flops / (us * 1e-6) / 1e12, 1)}
+        return out
+
+    res = {"workload": f"dense causal attention, B{b} H{h} N{n} D{d}, bf16, no documents",
+           "this_library": measure(lambda: SA.full_attention(q, k, v, scale))}
+    for name, be in (("torch_sdpa_efficient", SDPBackend.EFFICIENT_ATTENTION),
+                     ("torch_sdpa_flash", SDPBackend.FLASH_ATTENTION)):
+        try:
+            with sdpa_kernel(be):
+                res[name] = measure(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True))
+        except RuntimeError as e:  # the backend is not built for this device
+            res[name] = {"unavailable": str(e)[:120]}
+    return res
+
+
 def bench_c1(cfg, steps: int, cpu: bool):
     """C1 (SPS forward, B2 H8 D64, 1024 positions, w=64, one document per row, fp32 on the CPU). The
     reference's CPU paths on this host: (i) its CPU inference path, token by token through
@@ -601,7 +654,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work per baseline leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--no-other-configs", action="store_true", help="skip the C1, C2 and C4 lines")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the C1, C2 and C4 lines and the dense causal context")
     ap.add_argument("--profile-config", choices=("C2", "C3", "C4"),
                     help="run only this configuration's fwd+bwd steps and print its kernel timings (for profilers)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -652,6 +706,9 @@ def main() -> int:
             r.pop("doc_lengths", None)
             others[cfg.name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
             log(f"{cfg.name}: {r['value']:.1f} TFLOP/s, {r['ms_per_step']:.3f} ms/step, kernels {r['kernels']}")
+        log("dense causal context: this library vs torch scaled_dot_product_attention")
+        others["dense_causal"] = bench_dense_causal(10, args.warmup)
+        log(f"dense causal: {others['dense_causal']}")
         log("C1 forward (GPU) and the reference's CPU paths")
         others["C1"] = bench_c1(C1, args.steps, not args.no_cpu_baseline)
         log(f"C1: {others['C1']}")
