@@ -136,6 +136,8 @@ struct DmaTile {
   }
 
   // Element offset of row c32's chunk 2c + g (row-major fragment: 8 consecutive columns 16c + 8g).
+  // Both forms here and in frag_tr give the same offsets for the register-lean swizzle; each kernel
+  // keeps the form it was tuned with, since the compiler allocates registers differently for them.
   static __device__ __forceinline__ int frag(int c32, int g, int c) {
     if constexpr (kSpread)
       return c32 * D + ((2 * c + g) ^ swz(c32)) * 8;
