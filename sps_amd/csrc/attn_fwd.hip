@@ -177,6 +177,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
   if (planned) q_lanes(m, qp, run_start, st);
   float negm = 0.f;  // -m_run (0 while no score has been seen): the per-score FMA subtracts m_run
   float m_run = -INFINITY, l_run[4] = {0.f, 0.f, 0.f, 0.f};
+  // The rescale test in raw-score units: a pair's raw max above thr = (m_run + threshold) / scale2
+  // (any finite score while none has been seen) raises m_run, so the test is one compare per pair.
+  float thr = -INFINITY;
+  const float inv_scale2 = 1.f / scale2;
   f32x16_t acc[G::DC];
 #pragma unroll
   for (int dc = 0; dc < G::DC; ++dc) acc[dc] = f32x16_t{};
@@ -218,13 +222,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
           }
         }
       }
-      // The pair's max in scaled units (the max of the raw scores, times scale2 > 0). m_run is
-      // raised only past the lazy-rescale threshold (any score while none has been seen); the scores
-      // themselves stay raw, so a rescale touches only the accumulators, and they are scaled below
-      // by one FMA each, S * scale2 - m_run, in fp32.
-      const float mb = half_max(max32(sc[0], sc[1])) * scale2;
-      const bool need = m_run == -INFINITY ? mb > -INFINITY : mb - m_run > kRescaleThreshold;
+      // The pair's max of the raw scores (scaled units: times scale2 > 0). m_run is raised only past
+      // the lazy-rescale threshold; the scores themselves stay raw, so a rescale touches only the
+      // accumulators, and they are scaled below by one FMA each, S * scale2 - m_run, in fp32.
+      const float raw = half_max(max32(sc[0], sc[1]));
+      const bool need = raw > thr;
       if (wave_any(need)) {
+        const float mb = raw * scale2;
         const float m_new = need ? mb : m_run;
         const float alpha = need ? fast_exp2(m_run - m_new) : 1.f;
         m_run = m_new;
@@ -233,6 +237,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
 #pragma unroll
         for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
         negm = m_run == -INFINITY ? 0.f : -m_run;
+        thr = m_run == -INFINITY ? -INFINITY : (m_run + kRescaleThreshold) * inv_scale2;
       }
 #pragma unroll
       for (int y = 0; y < 2; ++y) {
