@@ -324,12 +324,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
   // dense swizzled tiles; smaller ones through registers into padded tiles.
   constexpr bool kDma = D >= 64;
   using DT = DmaTile<kDma ? D : 64, D != 256>;  // D = 256: the register-lean swizzle (fewer spills)
+  constexpr bool kSkew = D == 64 && NG == 4;
+  constexpr int kSkewMaxChunks = 16;
   constexpr int TE = kDma ? DT::ELEMS : G::ELEMS;
   __shared__ __attribute__((aligned(16))) uint16_t sQ[2][NG][TE];  // [buffer][chunk of the group]
   __shared__ __attribute__((aligned(16))) uint16_t sDO[2][NG][TE];
   // -LSE of the chunk's query rows in [0, kBlock), their -Delta in [kBlock, 2 kBlock).
   __shared__ __attribute__((aligned(16))) float sSeed[2][NG][2 * kBlock];
   __shared__ int s_span[2 * kWaves];
+  __shared__ int s_steps[kWaves];
 
   const MaskSpec m = a.m;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_index<D>();
@@ -349,6 +352,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
   const int nc = st.nc;
   const bool exact = row.mono;
   const int64_t dk_doc = (!exact && kvalid) ? load_doc(a, b, kp) : 0;
+  // Skewed schedule: wave w's keys start 2w chunks after the tile's first key, and a temporary-stream
+  // key with a short window sees only a few chunks, so waves sharing one 4-chunk group would each be
+  // busy in about half of it. Instead, at step s wave w takes chunk 2w + s: the eight staged chunks
+  // (both buffers, as one ring of slots) always hold chunks s .. s + 7, every wave has a block at
+  // each step, and one chunk enters the ring per step.
+  const bool skew = kSkew && st.stream == STREAM_TEMPORARY && nc > 0 && nc <= kSkewMaxChunks &&
+                    (stream_pos(m, st.stream, st.first) >> 5) == st.c0;
 
   const BufRsrc q_src = head_rsrc<D>(a.q + b * a.sq.b + h * a.sq.h, a.sq.n, m.N);
   const BufRsrc o_src = head_rsrc<D>(a.dO + b * a.sdo.b + h * a.sdo.h, a.sdo.n, m.N);
@@ -454,6 +464,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
       issue_dma(0, 0);
     else
       issue_regs(0, 0);
+    if constexpr (kSkew)
+      if (skew) issue_dma(1, 1);
     if (planned) k_lanes<kMono>(m, run_end, st);
     // The dP tile starts from the -Delta seeds of its query rows, so it comes out of the MFMAs as
     // dP - Delta and dS = P * dP' is one VALU operation per element; the S tile is scaled in fp32 by
@@ -462,15 +474,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
     auto cls_of = [&](int i) { return classify_block(st.w, (st.c0 + i) * kBlock, EXACT); };
     const BlockMask bm = k_block_mask(st, EXACT);
     // S and dP tiles of block y of the group (the dP tile starts from its rows' -Delta seeds).
-    auto sdp = [&](int y, int buf, f32x16_t& sc, f32x16_t& dp) {
-      const uint16_t* tQ = sQ[buf][y];
-      const uint16_t* tDO = sDO[buf][y];
+    auto sdp = [&](const uint16_t* tQ, const uint16_t* tDO, const float* seed, f32x16_t& sc, f32x16_t& dp) {
       sc = f32x16_t{};
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         // Query rows 8*i4 + 4g + {0..3} of this chunk.
         const f32x4_t d4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-            (const SPS_LDS float*)(&sSeed[buf][y][kBlock + 8 * i4 + 4 * g]));
+            (const SPS_LDS float*)(seed + kBlock + 8 * i4 + 4 * g));
 #pragma unroll
         for (int t = 0; t < 4; ++t) dp[4 * i4 + t] = d4[t];
       }
@@ -481,11 +491,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
       }
     };
     // Block y's S tile in fp32 (S * scale2 - LSE, the -LSE seeds read here), masked when partial.
-    auto scores = [&](int y, int buf, int qc, bool full, f32x16_t& sc) {
+    auto scores = [&](const float* seed, int qc, bool full, f32x16_t& sc) {
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const f32x4_t l4 = *reinterpret_cast<const SPS_LDS f32x4_t*>(
-            (const SPS_LDS float*)(&sSeed[buf][y][8 * i4 + 4 * g]));
+            (const SPS_LDS float*)(seed + 8 * i4 + 4 * g));
 #pragma unroll
         for (int t = 0; t < 4; ++t) sc[4 * i4 + t] = __builtin_fmaf(sc[4 * i4 + t], scale2, l4[t]);
       }
@@ -493,9 +503,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
         mask_partial<EXACT>(sc, st.r, st.w, qc, g, [&] { return ks_exact_bits(a, b, kp, st.r.hi, qc, g, dk_doc); });
     };
     // P and dS of block y, then the dV and dK products.
-    auto grads = [&](int y, int buf, const f32x16_t& sc, const f32x16_t& dp) {
-      const uint16_t* tQ = sQ[buf][y];
-      const uint16_t* tDO = sDO[buf][y];
+    auto grads = [&](const uint16_t* tQ, const uint16_t* tDO, const f32x16_t& sc, const f32x16_t& dp) {
       uint32_t pk[8], dsk[8];
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
@@ -522,19 +530,68 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
         }
       }
     };
+    auto block = [&](const uint16_t* tQ, const uint16_t* tDO, const float* seed, int qc, bool full) {
+      f32x16_t sc, dp;
+      sdp(tQ, tDO, seed, sc, dp);
+      scores(seed, qc, full, sc);
+      grads(tQ, tDO, sc, dp);
+    };
     auto body = [&](int j, int buf) {
       int act2, full2;
       group_codes<NG>(bm, NG * j, nc, cls_of, act2, full2);
 #pragma unroll
       for (int y = 0; y < NG; ++y) {
-        if ((act2 >> y) & 1) {
-          f32x16_t sc, dp;
-          sdp(y, buf, sc, dp);
-          scores(y, buf, (st.c0 + NG * j + y) * kBlock, (full2 >> y) & 1, sc);
-          grads(y, buf, sc, dp);
-        }
+        if ((act2 >> y) & 1) block(sQ[buf][y], sDO[buf][y], sSeed[buf][y], (st.c0 + NG * j + y) * kBlock, (full2 >> y) & 1);
       }
     };
+    if constexpr (kSkew) {
+      if (skew) {
+        // Chunk c sits in slot c % 8 = (buffer, chunk of the group) (c % 8 / 4, c % 4). Chunks 0-7
+        // were loaded by direct LDS loads before the lanes' setup; chunk s + 8 goes through
+        // registers during step s and is written at the start of step s + 1 into the slot of chunk
+        // s, which every wave has finished with by then (its last reader, wave 0, took it at step s).
+        uint16_t* const ringQ = &sQ[0][0][0];
+        uint16_t* const ringO = &sDO[0][0][0];
+        float* const ringS = &sSeed[0][0][0];
+        const uint64_t act = bm.act0, full = bm.full0;  // nc <= 16: every chunk's bit is in word 0
+        // Steps: until every wave has reached its last active chunk.
+        if (lane == 0) s_steps[wave] = (act ? 63 - __builtin_clzll(act) : -1) - 2 * wave + 1;
+        vmem_wait_all();
+        __syncthreads();
+        int steps = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) steps = imax(steps, s_steps[w]);
+        steps = wave_uniform(steps);
+        u32x4_t rq = {0u, 0u, 0u, 0u}, ro = {0u, 0u, 0u, 0u};
+        uint32_t rs = 0u;
+        for (int sp = 0; sp < steps; ++sp) {
+          if (sp > 0) {
+            const int c = sp + 7;
+            if (c < nc) {
+              const int sl = c & 7;
+              lds_write_b128(ringQ + sl * TE + tid * 8, rq);
+              lds_write_b128(ringO + sl * TE + tid * 8, ro);
+              if (wave == (c & 3)) ringS[sl * 2 * kBlock + lane] = __builtin_bit_cast(float, rs);
+            }
+          }
+          {
+            const int c = sp + 8;
+            if (c < nc) {
+              rq = buf_load_b128(q_src, q_c0 + (uint32_t)c * q_blk + q_dma.o[0]);
+              ro = buf_load_b128(o_src, o_c0 + (uint32_t)c * o_blk + o_dma.o[0]);
+              if (wave == (c & 3)) rs = __builtin_amdgcn_raw_buffer_load_b32(seed_src, seed_off(c), 0, 0);
+            }
+          }
+          const int i = 2 * wave + sp;
+          if (i < nc && ((act >> i) & 1ull)) {
+            const int sl = i & 7;
+            block(ringQ + sl * TE, ringO + sl * TE, ringS + sl * 2 * kBlock, (st.c0 + i) * kBlock, (full >> i) & 1ull);
+          }
+          lds_barrier();
+        }
+        return;
+      }
+    }
     if constexpr (kDma)
       run_groups_dma<NG, true>(nc, issue_dma, body);
     else
