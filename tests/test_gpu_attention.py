@@ -97,6 +97,12 @@ CASES = [
     ("reverse_sps", 2, 2, 512, 64, 64, "packed", None, torch.bfloat16, "bhnd"),
     ("reverse_sps", 1, 2, 340, 128, 17, None, 40, torch.float16, "bnhd"),
     ("reverse_sps", 1, 1, 200, 64, -1, "packed", None, torch.bfloat16, "bhnd"),
+    # D = 64 temporary-stream key tiles of at most 16 chunks take the skewed dK/dV schedule: with
+    # arbitrary (non-monotone) ids; at 16 chunks (window 128: a 128-key tile's queries span
+    # 2 (127 + 128) + 2 positions); at 17 chunks (window 130, the grouped schedule)
+    ("sps", 1, 2, 384, 64, 24, "random", None, torch.bfloat16, "bhnd"),
+    ("reverse_sps", 1, 2, 1024, 64, 128, "packed", None, torch.bfloat16, "bnhd"),
+    ("sps", 1, 1, 1024, 64, 130, None, None, torch.float16, "bhnd"),
     # head dim 256 (accepted by the reference's prefill asserts, triton_sps_flash_attention.py:510)
     ("full", 1, 2, 300, 256, 0, "packed", None, torch.bfloat16, "bhnd"),
     ("sps", 1, 2, 320, 256, 17, "packed", None, torch.float16, "bnhd"),
