@@ -20,16 +20,6 @@ constexpr int kRegIds = 8;  // ids per thread held in registers (rows up to kPre
 constexpr int kMaxSortTiles = 2048;  // rows with more tiles keep the closed-form order
 constexpr int kLdsRow = kPrepThreads * kRegIds;  // rows up to this length keep their runs in LDS
 
-// Run bounds of a position, from the LDS copy (rows up to kLdsRow) or from global memory.
-struct RunBounds {
-  const short* s_lds;
-  const short* e_lds;
-  const int* s_glb;
-  const int* e_glb;
-  __device__ __forceinline__ int start(int p) const { return s_lds ? s_lds[p] : s_glb[p]; }
-  __device__ __forceinline__ int end(int p) const { return e_lds ? e_lds[p] : e_glb[p]; }
-};
-
 // Exclusive scans of the per-thread chunk summaries, both in one pass so their latencies overlap:
 // a max-scan of `up` in thread order and a min-scan of `down` in reverse thread order. Inside each
 // wave: DPP shifts within the 16-lane rows (no LDS round trips), then the rows' totals from one lane
@@ -92,6 +82,17 @@ __device__ void block_exclusive_scans(int* s_up, int* s_down, int up, int down, 
   down_ex = imin(cd, ed);
 }
 
+// Minimum / maximum over each group of 8 consecutive lanes (all lanes active), held by every lane
+// of the group: quad swaps, then the half-row mirror.
+template <class Op>
+__device__ __forceinline__ int group8_reduce(int x, Op op) {
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));   // quad_perm [1, 0, 3, 2]
+  x = op(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));   // quad_perm [2, 3, 0, 1]
+  return op(x, __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false));  // row_half_mirror
+}
+__device__ __forceinline__ int group8_min(int x) { return group8_reduce(x, [](int u, int v) { return imin(u, v); }); }
+__device__ __forceinline__ int group8_max(int x) { return group8_reduce(x, [](int u, int v) { return imax(u, v); }); }
+
 // Ranks `n` <= kMaxSortTiles tiles by decreasing cost (ties: lower index first) and calls
 // emit(rank, tile) for each, with threads [first, first + count) of the workgroup (rank sort; the
 // cost reads are batched so their LDS latencies overlap).
@@ -134,10 +135,21 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   int64_t d[kRegIds];
   bool flag[kRegIds];
   if (in_regs) {
-    // Common case: every id of this thread's chunk (and its predecessor) loaded once, together.
-    const int64_t before = (p0 > 0 && p0 < N) ? load_doc(a, b, p0 - 1) : 0;
+    // Common case: every id of this thread's chunk (and its predecessor) loaded once, together: one
+    // branch on the id type around straight-line loads whose positions are clamped into the row
+    // (values past the chunk are never used), so all of them are in flight at once.
+    int64_t before = 0;
+    auto load_all = [&](auto* ids) {
+      ids += (int64_t)b * a.docs_sb;
+      const int64_t bv = ids[imax(imin(p0, N) - 1, 0)];
 #pragma unroll
-    for (int j = 0; j < kRegIds; ++j) d[j] = p0 + j < p1 ? load_doc(a, b, p0 + j) : 0;
+      for (int j = 0; j < kRegIds; ++j) d[j] = ids[imin(p0 + j, N - 1)];
+      before = (p0 > 0 && p0 < N) ? bv : 0;
+    };
+    if (a.docs_i64)
+      load_all(reinterpret_cast<const int64_t*>(a.docs));
+    else
+      load_all(reinterpret_cast<const int32_t*>(a.docs));
 #pragma unroll
     for (int j = 0; j < kRegIds; ++j) {
       const int p = p0 + j;
@@ -226,7 +238,6 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   }
   // Rows that fit read their run bounds from LDS (short: positions < kLdsRow <= 32767).
   const bool lds_ok = in_regs;
-  const RunBounds rb = {lds_ok ? s_start : nullptr, lds_ok ? s_end : nullptr, start, end};
 
   // Query-tile and key-tile plans, then both sorts. Rows with more than
   // kMaxSortTiles tiles keep the closed-form order (query tiles last to first, key tiles first to
@@ -237,41 +248,65 @@ __global__ __launch_bounds__(kPrepThreads) void row_layout_kernel(const AttnArgs
   TilePlan* qplan = a.q_plan + (int64_t)b * nqt;
   TilePlan* kplan = a.k_plan + (int64_t)b * nkt;
   const int mono_flag = mono ? 1 : 0;
-  auto st_of = [&](int q) { return rb.start(q); };
-  auto en_of = [&](int k) { return rb.end(k); };
-  // Query tiles are units [0, nqt), key tiles units [nqt, nqt + nkt); one thread per unit, each plan
-  // from the tile's first and last few rows (q_tile_union / k_tile_union).
-  for (int u = tid; u < nqt + nkt; u += kPrepThreads) {
-    if (u < nqt) {
-      const int t = u;
-      Interval u0, u1;
-      q_tile_union(m, t, st_of, u0, u1);
-      int b0, n0, b1, n1;
-      cover_blocks(u0.lo, u0.hi, b0, n0);
-      cover_blocks(u1.lo, u1.hi, b1, n1);
-      if (sort_q) {
-        s_cost[t] = n0 + n1;
-        s_qplan[t][0] = b0;
-        s_qplan[t][1] = n0;
-        s_qplan[t][2] = b1;
-        s_qplan[t][3] = n1;
+  // One 8-lane group per tile, one lane per row of the tile's first and last kTileEnds rows (the
+  // rows q_tile_union / k_tile_union take), the group's intervals combined by three DPP steps:
+  // query tiles on waves 0-7, key tiles on waves 8-15 (no wave runs both paths), 64 tiles per pass.
+  // The run bounds come from LDS or from global memory in two separate copies of the loop: with a
+  // global read anywhere in it, the loads' waits (vmcnt counts stores too) would also wait for the
+  // run-bound stores above.
+  static_assert(2 * kTileEnds == 8, "one lane of an 8-lane group per end row");
+  const bool key_half = tid >= kPrepThreads / 2;
+  const int lt = tid & (kPrepThreads / 2 - 1), grp = lt >> 3, row8 = lt & 7;
+  auto plans = [&](auto st_of, auto en_of) {
+    const int n = key_half ? nkt : nqt;
+    for (int t0 = 0; t0 < n; t0 += kPrepThreads / 16) {
+      const int t = t0 + grp;
+      if (!key_half) {
+        Interval i0 = {kEmptyLo, kEmptyHi}, i1 = i0;
+        const int q = t < n ? q_tile_row(m, t, row8) : -1;
+        if (q >= 0) query_intervals(m, q, st_of(q), i0, i1);
+        const Interval u0 = {group8_min(i0.lo), group8_max(i0.hi)}, u1 = {group8_min(i1.lo), group8_max(i1.hi)};
+        if (t < n && row8 == 0) {
+          int b0, n0, b1, n1;
+          cover_blocks(u0.lo, u0.hi, b0, n0);
+          cover_blocks(u1.lo, u1.hi, b1, n1);
+          if (sort_q) {
+            s_cost[t] = n0 + n1;
+            s_qplan[t][0] = b0;
+            s_qplan[t][1] = n0;
+            s_qplan[t][2] = b1;
+            s_qplan[t][3] = n1;
+          } else {
+            qplan[nqt - 1 - t] = TilePlan{t, mono_flag, b0, n0, b1, n1, 0, 0};
+          }
+        }
       } else {
-        qplan[nqt - 1 - t] = TilePlan{t, mono_flag, b0, n0, b1, n1, 0, 0};
-      }
-    } else {
-      const int t = u - nqt;
-      const Interval k = k_tile_union(m, t, en_of);
-      int c0, nc;
-      cover_blocks(k.lo, k.hi, c0, nc);
-      if (sort_k) {
-        s_cost_k[t] = nc;
-        s_kplan[t][0] = c0;
-        s_kplan[t][1] = nc;
-      } else {
-        kplan[t] = TilePlan{t, mono_flag, c0, nc, 0, 0, 0, 0};
+        Interval r = {kEmptyLo, kEmptyHi};
+        int stream = STREAM_NATURAL;
+        const int kp = t < n ? k_tile_row(m, t, row8, stream) : -1;
+        if (kp >= 0) {
+          const int last = key_last_query(m, stream, kp, en_of(kp));
+          if (last >= kp) r = Interval{kp, last};
+        }
+        const Interval k = {group8_min(r.lo), group8_max(r.hi)};
+        if (t < n && row8 == 0) {
+          int c0, nc;
+          cover_blocks(k.lo, k.hi, c0, nc);
+          if (sort_k) {
+            s_cost_k[t] = nc;
+            s_kplan[t][0] = c0;
+            s_kplan[t][1] = nc;
+          } else {
+            kplan[t] = TilePlan{t, mono_flag, c0, nc, 0, 0, 0, 0};
+          }
+        }
       }
     }
-  }
+  };
+  if (lds_ok)
+    plans([&](int q) { return (int)s_start[q]; }, [&](int k) { return (int)s_end[k]; });
+  else
+    plans([&](int q) { return start[q]; }, [&](int k) { return end[k]; });
   lds_barrier();  // the plans and costs are in LDS; the run-bound stores above keep draining
   if (sort_q)
     sort_tiles(s_cost, nqt, 0, kPrepThreads / 2, [&](int r, int t) {

@@ -125,14 +125,22 @@ __host__ __device__ __forceinline__ int key_last_query(const MaskSpec& m, int st
 // the tile does (tests/native/tile_plan_check.hip compares this with the union over every query).
 // start(q) is q's run start.
 constexpr int kTileEnds = 4;
+
+// Row j (< 2 kTileEnds) of query tile qt's first and last kTileEnds positions, or -1 past a short
+// tile's end.
+__host__ __device__ __forceinline__ int q_tile_row(const MaskSpec& m, int qt, int j) {
+  const int qa = qt * kTile, qz = imin(qa + kTile, m.N) - 1;
+  const int q = j < kTileEnds ? qa + j : qz - (j - kTileEnds);
+  return (q < qa || q > qz) ? -1 : q;
+}
+
 template <class StartFn>
 __host__ __device__ __forceinline__ void q_tile_union(const MaskSpec& m, int qt, StartFn start, Interval& u0,
                                                       Interval& u1) {
   u0 = u1 = Interval{kEmptyLo, kEmptyHi};
-  const int qa = qt * kTile, qz = imin(qa + kTile, m.N) - 1;
   for (int j = 0; j < 2 * kTileEnds; ++j) {
-    const int q = j < kTileEnds ? qa + j : qz - (j - kTileEnds);
-    if (q < qa || q > qz) continue;
+    const int q = q_tile_row(m, qt, j);
+    if (q < 0) continue;
     Interval i0, i1;
     query_intervals(m, q, start(q), i0, i1);  // an empty interval is {kEmptyLo, kEmptyHi}
     u0.lo = imin(u0.lo, i0.lo);
@@ -251,18 +259,25 @@ __host__ __device__ __forceinline__ void k_tile_run(const MaskSpec& m, int kt, i
   first = (kt < np ? kt : kt - np) * kTile;
 }
 
-// (Definition of k_tile_union, declared above.)
-template <class EndFn>
-__host__ __device__ __forceinline__ Interval k_tile_union(const MaskSpec& m, int kt, EndFn end) {
-  int stream, first;
+// Position of row j (< 2 kTileEnds) of key tile kt's first and last kTileEnds keys, or -1 past a
+// short tile's end; `stream` is the tile's key stream.
+__host__ __device__ __forceinline__ int k_tile_row(const MaskSpec& m, int kt, int j, int& stream) {
+  int first;
   k_tile_run(m, kt, stream, first);
   const int len = stream_len(m.family, m.N, stream, m.P);
   const int ta = first, tz = imin(first + kTile, len) - 1;
+  const int t = j < kTileEnds ? ta + j : tz - (j - kTileEnds);
+  return (t < ta || t > tz) ? -1 : stream_pos(m, stream, t);
+}
+
+// (Definition of k_tile_union, declared above.)
+template <class EndFn>
+__host__ __device__ __forceinline__ Interval k_tile_union(const MaskSpec& m, int kt, EndFn end) {
   Interval u{kEmptyLo, kEmptyHi};
   for (int j = 0; j < 2 * kTileEnds; ++j) {
-    const int t = j < kTileEnds ? ta + j : tz - (j - kTileEnds);
-    if (t < ta || t > tz) continue;
-    const int kp = stream_pos(m, stream, t);
+    int stream;
+    const int kp = k_tile_row(m, kt, j, stream);
+    if (kp < 0) continue;
     const int last = key_last_query(m, stream, kp, end(kp));
     if (last >= kp) {
       u.lo = imin(u.lo, kp);
