@@ -183,7 +183,10 @@ def bench_attention(cfg, steps: int, warmup: int, traffic: bool = False):
         return e0.elapsed_time(e1) / steps
 
     dq_call()  # the dK/dV pass reads the seeds the dQ pass writes
-    fwd_ms, dq_ms, dkdv_ms = per_launch_ms(fwd_call), per_launch_ms(dq_call), per_launch_ms(dkdv_call)
+    # Each pass's time per launch: the median over five rounds (the passes interleaved), each round
+    # `steps` launches back to back between two events.
+    rounds = [(per_launch_ms(fwd_call), per_launch_ms(dq_call), per_launch_ms(dkdv_call)) for _ in range(5)]
+    fwd_ms, dq_ms, dkdv_ms = (statistics.median(r[i] for r in rounds) for i in range(3))
     ms_per_step = wall / steps * 1e3
     flops = useful_flops(cfg, lengths)
     d = cfg.head_dim
