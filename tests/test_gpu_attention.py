@@ -103,6 +103,7 @@ CASES = [
     ("sps", 1, 2, 384, 64, 24, "random", None, torch.bfloat16, "bhnd"),
     ("reverse_sps", 1, 2, 1024, 64, 128, "packed", None, torch.bfloat16, "bnhd"),
     ("sps", 1, 1, 1024, 64, 130, None, None, torch.float16, "bhnd"),
+    ("sps", 2, 1, 512, 64, 40, "packed", None, torch.float16, "bnhd"),
     # head dim 256 (accepted by the reference's prefill asserts, triton_sps_flash_attention.py:510)
     ("full", 1, 2, 300, 256, 0, "packed", None, torch.bfloat16, "bhnd"),
     ("sps", 1, 2, 320, 256, 17, "packed", None, torch.float16, "bnhd"),
