@@ -85,6 +85,9 @@ def cpu_info() -> dict:
 # HBM traffic per launch (from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this script)
 # ----------------------------------------------------------------------------------------------
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_c3_c5.txt"
+# The same counters over the C2 and C4 steps (bench.py --profile-config C2 / C4).
+TRAFFIC_FILES = {"C3": TRAFFIC_FILE, "C2": ROOT / "profiles" / "hbm_traffic_c2.txt",
+                 "C4": ROOT / "profiles" / "hbm_traffic_c4.txt"}
 
 
 def copy_probe(mib: int) -> None:
@@ -101,12 +104,12 @@ def copy_probe(mib: int) -> None:
     del src, dst
 
 
-def recorded_traffic() -> dict:
-    """Calibrated HBM bytes per launch of each kernel, as recorded in TRAFFIC_FILE (lines
+def recorded_traffic(path: Path = TRAFFIC_FILE) -> dict:
+    """Calibrated HBM bytes per launch of each kernel, as recorded in `path` (lines
     `<kernel> fetch_bytes=<n> write_bytes=<n>`); empty when the file is absent."""
     out = {}
     try:
-        text = TRAFFIC_FILE.read_text()
+        text = path.read_text()
     except OSError:
         return out
     for line in text.splitlines():
@@ -216,8 +219,9 @@ def bench_attention(cfg, steps: int, warmup: int, traffic: bool = False):
                            "algorithmic_gflop": round(x["flop"] / 1e9, 3)} for name, x in kernels.items()},
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(dk["tflops"], 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dk["frac"], 4),
-                     # The recorded traffic is of the C3 workload's launches.
-                     "traffic": recorded_traffic().get(dominant) if traffic else None},
+                     # Recorded counter traffic of this configuration's launches.
+                     "traffic": recorded_traffic(TRAFFIC_FILES[cfg.name]).get(dominant)
+                     if traffic and cfg.name in TRAFFIC_FILES else None},
     }
 
 
@@ -684,6 +688,9 @@ def main() -> int:
     from sps_amd.workloads import C1, C2, C3, C4, C5
 
     _native.lib()
+    if args.copy_probe_mib > 0:
+        log(f"copy probe: torch.neg over {args.copy_probe_mib} MiB fp32, 3 launches")
+        copy_probe(args.copy_probe_mib)
     if args.profile_config:
         cfg = {"C2": C2, "C3": C3, "C4": C4}[args.profile_config]
         log(f"{cfg.name} fwd+bwd only: {args.warmup} warm-up + {args.steps} timed steps")
@@ -691,9 +698,6 @@ def main() -> int:
         print(json.dumps({"config": cfg.name, "value": round(r["value"], 3), "unit": "TFLOP/s",
                           "ms_per_step": round(r["ms_per_step"], 4), "kernels": r["kernels"]}), flush=True)
         return 0
-    if args.copy_probe_mib > 0:
-        log(f"copy probe: torch.neg over {args.copy_probe_mib} MiB fp32, 3 launches")
-        copy_probe(args.copy_probe_mib)
     log(f"C3 fwd+bwd: {args.warmup} warm-up + {args.steps} timed steps")
     att = bench_attention(C3, args.steps, args.warmup, traffic=True)
     log(f"C3: {att['value']:.1f} TFLOP/s, {att['ms_per_step']:.3f} ms/step, kernels {att['kernels']}")
@@ -705,7 +709,7 @@ def main() -> int:
     if not args.no_other_configs:
         for cfg in (C2, C4):
             log(f"{cfg.name} fwd+bwd: {args.warmup} warm-up + {args.steps} timed steps")
-            r = bench_attention(cfg, args.steps, args.warmup)
+            r = bench_attention(cfg, args.steps, args.warmup, traffic=True)
             r.pop("doc_lengths", None)
             others[cfg.name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
             log(f"{cfg.name}: {r['value']:.1f} TFLOP/s, {r['ms_per_step']:.3f} ms/step, kernels {r['kernels']}")
