@@ -41,3 +41,18 @@ def test_visible_pairs_match_oracle_counts(name):
 def test_headline_flops():
     # C3 fwd+bwd useful work, 14 * D per visible pair over 16 heads (the bench's metric denominator).
     assert round(W.useful_flops(W.C3, FIXTURE["C3"]["lengths"]) / 1e9, 3) == 89.232
+
+
+def test_recorded_traffic_covers_every_attention_config():
+    # The bench line's roofline.traffic for C2, C3 and C4 comes from the committed counter summaries;
+    # each must give fetch + write bytes for every attention kernel, at least the kernel's compulsory
+    # traffic (K and V read, dK and dV written once: 4 B*H*N*D*2 bytes).
+    import bench
+
+    for name in ("C2", "C3", "C4"):
+        cfg = getattr(W, name)
+        t = bench.recorded_traffic(bench.TRAFFIC_FILES[name])
+        for kernel in ("row_layout_kernel", "attn_fwd_kernel", "attn_bwd_dq_kernel", "attn_bwd_dkdv_kernel"):
+            assert t.get(kernel, 0) > 0, (name, kernel)
+        compulsory = 4 * cfg.batch * cfg.heads * cfg.n * cfg.head_dim * 2
+        assert t["attn_bwd_dkdv_kernel"] >= compulsory, name
