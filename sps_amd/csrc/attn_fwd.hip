@@ -41,8 +41,21 @@ constexpr float kRescaleThreshold = 8.0f;
 // loaded from here reads as zeros.
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
-template <int D, class E>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : (D <= 128 ? 2 : 1), 8))) void attn_fwd_kernel(const AttnArgs a) {
+// Waves per SIMD the forward is compiled for. At D = 64 the SPS families run four (their per-wave
+// loops are short, so more resident waves hide more of each workgroup's setup: C3 forward -5 %
+// against three), full attention three (four measured +4 % at C2, whose longer loops gain less
+// from it than they lose to the tighter register budget).
+template <int D>
+constexpr int fwd_waves_full() {
+  return D <= 64 ? 3 : (D <= 128 ? 2 : 1);
+}
+template <int D>
+constexpr int fwd_waves_sps() {
+  return D == 64 ? 4 : fwd_waves_full<D>();
+}
+
+template <int D, class E, int W>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, 8))) void attn_fwd_kernel(const AttnArgs a) {
   using G = TileGeom<D>;
   // Head dims of 64 and more stage K / V blocks by direct global -> LDS loads into dense swizzled
   // tiles (no staging registers, no LDS write instructions); smaller ones through registers into
@@ -185,10 +198,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
 #pragma unroll
   for (int dc = 0; dc < G::DC; ++dc) acc[dc] = f32x16_t{};
 
-  // One pair = two 32-row key blocks: both score tiles, one joint max / rescale decision, PV for both.
-  // The score tiles are computed for both blocks whenever the pair has work for this wave (a skipped
-  // block is masked to -inf instead of branched around), and masks run only in pairs that have a
-  // partial block: few branches, so the compiler can interleave the MFMA and VALU work.
+  // One pair = two 32-row key blocks staged together (one barrier per pair); the softmax runs block
+  // by block (score tile, mask if partial, max / rescale decision, exponentials and PV), so only one
+  // 16-register score tile is live: against both tiles and one joint decision per pair, 40 fewer
+  // VGPRs, which is what lets D = 64 run four waves per SIMD.
   auto run = [&](auto exact_tag) {
     constexpr bool EXACT = decltype(exact_tag)::value;
     auto cls_of = [&](int i) {
@@ -199,53 +212,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3
       int act2, full2;
       pair_codes(bm, 2 * j, nb, cls_of, act2, full2);
       if (act2 == 0) return;
-      f32x16_t sc[2];
 #pragma unroll
       for (int y = 0; y < 2; ++y) {
+        if (!((act2 >> y) & 1)) continue;
         const uint16_t* kt = tK(buf, y);
-        sc[y] = E::mfma(row_frag(kt, 0), qf[0], f32x16_t{});
+        f32x16_t sc = E::mfma(row_frag(kt, 0), qf[0], f32x16_t{});
 #pragma unroll
-        for (int c = 1; c < D / 16; ++c) sc[y] = E::mfma(row_frag(kt, c), qf[c], sc[y]);
-      }
-      if (full2 != 3) {
-#pragma unroll
-        for (int y = 0; y < 2; ++y) {
-          if (!((act2 >> y) & 1)) {
-            sc[y] = f32x16_t{} - INFINITY;
-          } else if (!((full2 >> y) & 1)) {
-            const int i = 2 * j + y;
-            const bool s0 = i < plan.n0;
-            const int t0 = plan.first(i);
-            const Interval lr = s0 ? st.r0 : st.r1;
-            mask_partial<EXACT>(sc[y], lr, s0 ? st.w0 : st.w1, t0, g,
-                                [&] { return qs_exact_bits(a, b, lr, plan.stream(i), t0, g, dq_doc); });
-          }
+        for (int c = 1; c < D / 16; ++c) sc = E::mfma(row_frag(kt, c), qf[c], sc);
+        if (!((full2 >> y) & 1)) {
+          const int i = 2 * j + y;
+          const bool s0 = i < plan.n0;
+          const int t0 = plan.first(i);
+          const Interval lr = s0 ? st.r0 : st.r1;
+          mask_partial<EXACT>(sc, lr, s0 ? st.w0 : st.w1, t0, g,
+                              [&] { return qs_exact_bits(a, b, lr, plan.stream(i), t0, g, dq_doc); });
         }
-      }
-      // The pair's max of the raw scores (scaled units: times scale2 > 0). m_run is raised only past
-      // the lazy-rescale threshold; the scores themselves stay raw, so a rescale touches only the
-      // accumulators, and they are scaled below by one FMA each, S * scale2 - m_run, in fp32.
-      const float raw = half_max(max32(sc[0], sc[1]));
-      const bool need = raw > thr;
-      if (wave_any(need)) {
-        const float mb = raw * scale2;
-        const float m_new = need ? mb : m_run;
-        const float alpha = need ? fast_exp2(m_run - m_new) : 1.f;
-        m_run = m_new;
+        // The block's max of the raw scores (scaled units: times scale2 > 0). m_run is raised only
+        // past the lazy-rescale threshold; the scores themselves stay raw, so a rescale touches only
+        // the accumulators, and they are scaled below by one FMA each, S * scale2 - m_run, in fp32.
+        float mx = max3f(sc[0], sc[1], sc[2]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) l_run[r] *= alpha;
+        for (int e = 3; e < 15; e += 2) mx = max3f(mx, sc[e], sc[e + 1]);
+        mx = __builtin_elementwise_maximum(mx, sc[15]);
+        const float raw = half_max(mx);
+        const bool need = raw > thr;
+        if (wave_any(need)) {
+          const float mb = raw * scale2;
+          const float m_new = need ? mb : m_run;
+          const float alpha = need ? fast_exp2(m_run - m_new) : 1.f;
+          m_run = m_new;
 #pragma unroll
-        for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
-        negm = m_run == -INFINITY ? 0.f : -m_run;
-        thr = m_run == -INFINITY ? -INFINITY : (m_run + kRescaleThreshold) * inv_scale2;
-      }
+          for (int r = 0; r < 4; ++r) l_run[r] *= alpha;
 #pragma unroll
-      for (int y = 0; y < 2; ++y) {
+          for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
+          negm = m_run == -INFINITY ? 0.f : -m_run;
+          thr = m_run == -INFINITY ? -INFINITY : (m_run + kRescaleThreshold) * inv_scale2;
+        }
         uint32_t pk[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float p0 = fast_exp2(__builtin_fmaf(sc[y][2 * e], scale2, negm));
-          const float p1 = fast_exp2(__builtin_fmaf(sc[y][2 * e + 1], scale2, negm));
+          const float p0 = fast_exp2(__builtin_fmaf(sc[2 * e], scale2, negm));
+          const float p1 = fast_exp2(__builtin_fmaf(sc[2 * e + 1], scale2, negm));
           pk[e] = E::pack2(p0, p1);
           l_run[e & 3] = E::sum2(pk[e], l_run[e & 3]);  // four independent partial sums
         }
@@ -351,7 +358,10 @@ template <int D, class E>
 static hipError_t launch_fwd_t(const AttnArgs& a, hipStream_t stream) {
   const int64_t nblocks = (int64_t)q_tiles(a.m.N) * a.B * a.H;
   if (nblocks == 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, E>), dim3((unsigned)nblocks), dim3(256), 0, stream, a);
+  if (a.m.family == FAMILY_FULL)
+    hipLaunchKernelGGL((attn_fwd_kernel<D, E, fwd_waves_full<D>()>), dim3((unsigned)nblocks), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<D, E, fwd_waves_sps<D>()>), dim3((unsigned)nblocks), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
