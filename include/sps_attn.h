@@ -78,13 +78,14 @@ int sps_last_error(char* buf, size_t len);
 size_t sps_attn_workspace_bytes(int family, int B, int H, int N, int has_docs, int backward);
 
 /*
- * Forward attention. q, k, v, o: [B, H, N, D] of dtype (bf16 or f16), D in {16, 32, 64, 128}.
+ * Forward attention. q, k, v, o: [B, H, N, D] of dtype (bf16 or f16), D in {16, 32, 64, 128, 256}.
  * lse: [B, H, N] fp32 contiguous, receives the log2-domain log-sum-exp of the scaled scores
  * (m + log2 l), consumed by sps_attn_bwd. docs may be NULL (no document mask).
  * window: temporary-key window in tokens (SPS families). has_pkw/pkw: optional persistent-key
- * window (the reference's persistent_key_window; has_pkw = 0 means None). sm_scale may be any value:
- * the kernels form S * sm_scale * log2(e) in fp32 from the unscaled 16-bit inputs, as the reference
- * scales its fp32 scores.
+ * window (the reference's persistent_key_window; has_pkw = 0 means None). sm_scale may be any finite
+ * value (zero and negative ones too; NaN or infinity: SPS_E_INVALID): the kernels form
+ * S * sm_scale * log2(e) in fp32 from the unscaled 16-bit inputs, as the reference scales its fp32
+ * scores. fp32 inputs are not taken (SPS_E_UNSUPPORTED): the path runs on bf16/f16 MFMA only.
  */
 int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype,
                  const void* q, const int64_t* q_strides,

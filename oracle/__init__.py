@@ -2,7 +2,8 @@
 
 This package restates, on the CPU, the algorithms of the reference (lil-lab/sps) for the attention
 path: the visibility predicate (C, ``sps_oracle.c``, and an independent numpy form), dense masked
-attention forward/backward (numpy, float64), segmented decode attention (numpy, float64), document
+attention forward/backward (numpy, float64), an emulation of the reference kernels' own 16-bit
+arithmetic (torch CPU, float32: ``emulate.py``), segmented decode attention (numpy, float64), document
 ids (numpy), and a torch-CPU port of the reference's CPU fallback path used as the timed CPU
 baseline. Each function cites the reference file:line it follows.
 
@@ -22,4 +23,7 @@ Pinning (what makes each function trustworthy; see tests/test_oracle_*.py):
                            the closed form of a ring after n inserts (insert i in slot i mod W,
                            len = min(n, W), pos = n mod W once full), retained append up to storage.
   document ids           — reference KATs (core/test_document_idx.py).
+  emulate (the reference — with rounding off it equals the float64 dense attention for every family,
+   kernels' 16-bit         block size and mask; with float32 as the "16-bit" type it is fp32-accurate;
+   arithmetic)             uniform scores give the closed form (mean of V, M = log2 count).
 """

@@ -172,8 +172,11 @@ def attention_backward(do, q, k, v, o, lse, sm_scale, family, window=0, document
 # The attention as torch.library custom ops, so a torch.compile'd model (the reference trains with
 # torch.compile, scripts/train.py:420-422) traces it as two opaque calls without a graph break. The
 # forward returns its outputs and, when a backward will follow and documents are given, the
-# workspace holding the document row layout; the backward reuses that layout and writes its -LSE /
-# -Delta seeds into the same workspace (declared as mutated).
+# workspace holding the document row layout; the backward reads that layout. It also writes its
+# -LSE / -Delta seeds into the workspace's seed region, which is scratch: the backward writes it
+# before reading it, and nothing else reads it, so the op's results depend on its inputs only and
+# the op is declared pure. (Declaring the workspace mutated would bump the version of the tensor
+# the forward saved, and a second backward over a retained graph would then be refused.)
 @torch.library.custom_op("sps_amd::attention_fwd", mutates_args=())
 def _attention_fwd_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, docs: Optional[torch.Tensor],
                       sm_scale: float, family: int, window: int, pkw: Optional[int],
@@ -195,7 +198,7 @@ def _(q, k, v, docs, sm_scale, family, window, pkw, keep_layout):
     return o, lse, q.new_empty((nbytes,), dtype=torch.uint8)
 
 
-@torch.library.custom_op("sps_amd::attention_bwd", mutates_args=("ws",))
+@torch.library.custom_op("sps_amd::attention_bwd", mutates_args=())
 def _attention_bwd_op(do: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                       lse: torch.Tensor, docs: Optional[torch.Tensor], ws: torch.Tensor, sm_scale: float, family: int,
                       window: int, pkw: Optional[int]) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:

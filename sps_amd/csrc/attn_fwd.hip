@@ -17,13 +17,15 @@
 // the end of the sequence read as zeros.
 //
 // Softmax: exp2 domain. The score MFMAs deliver S = K Q^T in fp32 from the unscaled inputs, and one
-// FMA per score forms S * sm_scale * log2(e) - m_run in fp32, as the reference scales its fp32 scores
-// (triton_sps_flash_attention.py:78-79): scaling an input operand instead would round Q * scale to
-// the input type, an error that grows with the score magnitude. Masks are applied to the scaled
-// scores, so any scale (zero or negative too) keeps masked keys at -inf. The running max is only
-// raised (and the accumulator rescaled) when a block's max exceeds it by more than 2^8, so P stays
-// <= 256 and most blocks skip the rescale; row sums of P use v_dot2 on the packed 16-bit P the MFMA
-// consumes.
+// FMA per score forms S * scale2 - m_run in fp32 (scale2 = sm_scale * log2 e), as the reference
+// scales its fp32 scores (triton_sps_flash_attention.py:78-79): scaling an input operand instead would
+// round Q * scale to the input type, an error that grows with the score magnitude. Masked scores are
+// set to -inf while still raw, and the running max is taken over the raw scores (times scale2), so
+// scale2 must be positive: a negative sm_scale flips the sign bits of Q instead (exact in 16 bits),
+// and a zero one is replaced by 2^-100 (every visible score then scales to within 2^-80 of 0, while
+// masked ones stay -inf). The running max is only raised (and the accumulator rescaled) when a
+// block's max exceeds it by more than 2^8, so P stays <= 256 and most blocks skip the rescale; row
+// sums of P use v_dot2 on the packed 16-bit P the MFMA consumes.
 //
 // Reference semantics: _attn_fwd_sps / _attn_fwd_inner_sps (triton_sps_flash_attention.py:26-269),
 // _attn_fwd (triton_reverse_sps_flash_attention.py:242-331, triton_full_flash_attention.py:204-283):

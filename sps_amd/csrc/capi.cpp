@@ -170,6 +170,9 @@ int sps_attn_fwd(int family, int B, int H, int N, int D, int dtype, const void* 
   if (!supported_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "head_dim %d not supported", D);
   if (dtype != SPS_DTYPE_BF16 && dtype != SPS_DTYPE_F16)
     return fail(SPS_E_UNSUPPORTED, "attention dtype code %d not supported (bf16, f16)", dtype);
+  // Any finite scale is taken (zero and negative ones too); a NaN or infinite one would leave the
+  // softmax undefined.
+  if (!std::isfinite(sm_scale)) return fail(SPS_E_INVALID, "sm_scale must be finite");
   const int need = (int64_t)B * H * N > 0;
   if ((rc = check_tensor("q", q, q_strides, need, N, D)) || (rc = check_tensor("k", k, k_strides, need, N, D)) ||
       (rc = check_tensor("v", v, v_strides, need, N, D)) || (rc = check_tensor("o", o, o_strides, need, N, D)))
@@ -211,6 +214,9 @@ static int attn_bwd_impl(int passes, int family, int B, int H, int N, int D, int
   if (!supported_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "head_dim %d not supported", D);
   if (dtype != SPS_DTYPE_BF16 && dtype != SPS_DTYPE_F16)
     return fail(SPS_E_UNSUPPORTED, "attention dtype code %d not supported (bf16, f16)", dtype);
+  // Any finite scale is taken (zero and negative ones too); a NaN or infinite one would leave the
+  // softmax undefined.
+  if (!std::isfinite(sm_scale)) return fail(SPS_E_INVALID, "sm_scale must be finite");
   const int need = (int64_t)B * H * N > 0;
   if ((rc = check_tensor("q", q, q_strides, need, N, D)) || (rc = check_tensor("k", k, k_strides, need, N, D)) ||
       (rc = check_tensor("v", v, v_strides, need, N, D)) || (rc = check_tensor("o", o, o_strides, need, N, D)) ||

@@ -75,21 +75,27 @@ _HOME = {
 }
 
 # Consumer module -> names it binds at import time.
+# (sps/core.py looks apply_rotary_emb up in modeling.models.model at call time, :50; the others
+# import it by name: full_attention_model.py:26-32, reverse_sps/core.py:16-19,
+# reverse_sps/inference.py:13-14.)
 _CONSUMERS = {
     "modeling.models.sps.core": {"triton_sps_sliding_attention": _attn.sps_sliding_attention},
     "modeling.models.reverse_sps.core": {
         "triton_reverse_sps_sliding_attention": _attn.reverse_sps_sliding_attention,
+        "apply_rotary_emb": None,
         "generate_left_padded_document_idx": None,
     },
     "modeling.models.full_attention_model": {
         "triton_full_attention": _attn.full_attention,
         "KVSegment": _dec.KVSegment,
         "masked_kv_attention": None,
+        "apply_rotary_emb": None,
         "generate_left_padded_document_idx": None,
     },
     "modeling.models.reverse_sps.inference": {
         "KVSegment": _dec.KVSegment,
         "masked_kv_attention": None,
+        "apply_rotary_emb": None,
         "triton_segmented_q2_attention": _dec.triton_segmented_q2_attention,
         "fused_sps_kv_update": _fast.fused_sps_kv_update,
     },

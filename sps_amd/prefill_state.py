@@ -47,16 +47,23 @@ def prefill_to_decode(k_Bx2TxHxD: Tensor, v_Bx2TxHxD: Tensor, current_doc_mask_B
     assert br_len.dtype in _LEN_DTYPES and (not use_ring or (nw_len.dtype == br_len.dtype and nw_pos.dtype == br_len.dtype))
     assert d % 8 == 0, f"head_dim {d} must be a multiple of 8"
     assert k_Bx2TxHxD.is_cuda and br_k.is_cuda, "prefill_to_decode: tensors must be on the GPU"
-    # The reference's slice assignment fails when a document does not fit the retained buffer.
-    doc_len = current_doc_mask_BxT.sum(dim=1)
-    if b and int(doc_len.max()) > br_k.size(2):
-        raise RuntimeError(f"a prompt document of {int(doc_len.max())} tokens does not fit the retained buffer "
-                           f"({br_k.size(2)} rows)")
+    # The reference's slice assignment fails when a document does not fit the retained buffer. A
+    # document has at most T tokens, so with a buffer of T rows or more this is a shape check; only a
+    # shorter buffer needs the lengths read back (a host sync).
+    if b and br_k.size(2) < t:
+        longest = int(current_doc_mask_BxT.sum(dim=1).max())
+        if longest > br_k.size(2):
+            raise RuntimeError(f"a prompt document of {longest} tokens does not fit the retained buffer "
+                               f"({br_k.size(2)} rows)")
     k = k_Bx2TxHxD if _aligned(k_Bx2TxHxD) else k_Bx2TxHxD.contiguous()
     v = v_Bx2TxHxD if _aligned(v_Bx2TxHxD) else v_Bx2TxHxD.contiguous()
     for c in (br_k, br_v) + ((nw_k, nw_v) if use_ring else ()):
         assert _aligned(c), "KV caches must have 16-byte aligned rows"
-    mask = current_doc_mask_BxT.to(torch.uint8).contiguous()
+    # A bool mask with unit column stride is read in place (one byte per flag, 0 or 1).
+    if current_doc_mask_BxT.dtype == torch.bool and current_doc_mask_BxT.stride(1) == 1:
+        mask = current_doc_mask_BxT.view(torch.uint8)
+    else:
+        mask = current_doc_mask_BxT.to(torch.uint8).contiguous()
     cs = lambda x, y: N.i64_array((x.stride(0), x.stride(1), x.stride(2), y.stride(0), y.stride(1), y.stride(2)))  # noqa: E731
     if use_ring:
         ring = (nw_k.data_ptr(), nw_v.data_ptr(), cs(nw_k, nw_v), nw_k.size(2), window_tokens, nw_len.data_ptr(),

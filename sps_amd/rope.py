@@ -69,45 +69,68 @@ def _launch(q: Tensor, k: Tensor, v: Optional[Tensor], freqs_cis: Tensor, q_out:
     N.check("sps_rope_qkv", status)
 
 
-class _RopePair(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, xq, xk, freqs_cis):
-        q_out = torch.empty(xq.shape, device=xq.device, dtype=xq.dtype)
-        k_out = torch.empty(xk.shape, device=xk.device, dtype=xk.dtype)
-        _launch(xq, xk, None, freqs_cis, q_out, k_out, None)
-        ctx.save_for_backward(freqs_cis)
-        return q_out, k_out
-
-    @staticmethod
-    def backward(ctx, gq, gk):
-        (freqs_cis,) = ctx.saved_tensors
-        ref = gq if gq is not None else gk
-        gq = gq if gq is not None else torch.zeros_like(ref)
-        gk = gk if gk is not None else torch.zeros_like(ref)
-        dq = torch.empty(gq.shape, device=gq.device, dtype=gq.dtype)
-        dk = torch.empty(gk.shape, device=gk.device, dtype=gk.dtype)
-        _launch(gq, gk.to(gq.dtype), None, _conj(freqs_cis), dq, dk, None)
-        return dq, dk, None
+# Both functions as torch.library custom ops with fake implementations and registered autograd, so a
+# torch.compile'd model (the reference trains compiled, scripts/train.py:420-422; sps/core.py:50-52
+# calls apply_rotary_emb inside the compiled forward) traces them without a graph break. The
+# backward of each is the same op on the incoming gradients with the conjugate frequencies, cast
+# back to the input dtype.
+@torch.library.custom_op("sps_amd::rope_pair", mutates_args=())
+def _rope_pair_op(xq: Tensor, xk: Tensor, freqs_cis: Tensor) -> Tuple[Tensor, Tensor]:
+    q_out = torch.empty(xq.shape, device=xq.device, dtype=xq.dtype)
+    k_out = torch.empty(xk.shape, device=xk.device, dtype=xk.dtype)
+    _launch(xq, xk, None, freqs_cis, q_out, k_out, None)
+    return q_out, k_out
 
 
-class _RopeQKV(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, k, v, freqs_cis, out_dtype):
-        outs = [torch.empty(q.shape, device=q.device, dtype=out_dtype) for _ in range(3)]
-        _launch(q, k, v, freqs_cis, *outs)
-        ctx.save_for_backward(freqs_cis)
-        ctx.in_dtype = q.dtype
-        return tuple(outs)
+@_rope_pair_op.register_fake
+def _(xq, xk, freqs_cis):
+    return torch.empty_like(xq, memory_format=torch.contiguous_format), torch.empty_like(
+        xk, memory_format=torch.contiguous_format)
 
-    @staticmethod
-    def backward(ctx, gq, gk, gv):
-        (freqs_cis,) = ctx.saved_tensors
-        ref = next(g for g in (gq, gk, gv) if g is not None)
-        gq, gk, gv = (g if g is not None else torch.zeros_like(ref) for g in (gq, gk, gv))
-        dt = gq.dtype
-        outs = [torch.empty(gq.shape, device=gq.device, dtype=ctx.in_dtype) for _ in range(3)]
-        _launch(gq, gk.to(dt), gv.to(dt), _conj(freqs_cis), *outs)
-        return outs[0], outs[1], outs[2], None, None
+
+def _rope_pair_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[2])
+
+
+def _rope_pair_backward(ctx, gq, gk):
+    (freqs_cis,) = ctx.saved_tensors
+    ref = gq if gq is not None else gk
+    gq = gq if gq is not None else torch.zeros_like(ref)
+    gk = gk if gk is not None else torch.zeros_like(ref)
+    dq, dk = torch.ops.sps_amd.rope_pair(gq, gk, _conj(freqs_cis))
+    return dq, dk, None
+
+
+_rope_pair_op.register_autograd(_rope_pair_backward, setup_context=_rope_pair_setup)
+
+
+@torch.library.custom_op("sps_amd::rope_qkv", mutates_args=())
+def _rope_qkv_op(q: Tensor, k: Tensor, v: Tensor, freqs_cis: Tensor,
+                 out_dtype: torch.dtype) -> Tuple[Tensor, Tensor, Tensor]:
+    outs = [torch.empty(q.shape, device=q.device, dtype=out_dtype) for _ in range(3)]
+    _launch(q, k, v, freqs_cis, *outs)
+    return tuple(outs)
+
+
+@_rope_qkv_op.register_fake
+def _(q, k, v, freqs_cis, out_dtype):
+    return tuple(torch.empty(q.shape, device=q.device, dtype=out_dtype) for _ in range(3))
+
+
+def _rope_qkv_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[3])
+    ctx.in_dtype = inputs[0].dtype
+
+
+def _rope_qkv_backward(ctx, gq, gk, gv):
+    (freqs_cis,) = ctx.saved_tensors
+    ref = next(g for g in (gq, gk, gv) if g is not None)
+    gq, gk, gv = (g if g is not None else torch.zeros_like(ref) for g in (gq, gk, gv))
+    dq, dk, dv = torch.ops.sps_amd.rope_qkv(gq, gk.to(gq.dtype), gv.to(gq.dtype), _conj(freqs_cis), ctx.in_dtype)
+    return dq, dk, dv, None, None
+
+
+_rope_qkv_op.register_autograd(_rope_qkv_backward, setup_context=_rope_qkv_setup)
 
 
 def _conj(freqs_cis: Tensor) -> Tensor:
@@ -117,7 +140,7 @@ def _conj(freqs_cis: Tensor) -> Tensor:
 def apply_rotary_emb(xq: Tensor, xk: Tensor, freqs_cis: Tensor) -> Tuple[Tensor, Tensor]:
     """RoPE on [B, T, H, D] queries and keys; returns new tensors of the inputs' dtype and shape."""
     assert xq.ndim == 4 and xk.shape == xq.shape
-    return _RopePair.apply(xq, xk, freqs_cis)
+    return torch.ops.sps_amd.rope_pair(xq, xk, freqs_cis)
 
 
 def rope_qkv_for_attention(q: Tensor, k: Tensor, v: Tensor, freqs_cis: Tensor,
@@ -128,5 +151,5 @@ def rope_qkv_for_attention(q: Tensor, k: Tensor, v: Tensor, freqs_cis: Tensor,
     full_attention."""
     assert q.ndim == 4 and k.shape == q.shape and v.shape == q.shape
     assert out_dtype in _FLOAT_DTYPES
-    outs = _RopeQKV.apply(q, k, v, freqs_cis, out_dtype)
+    outs = torch.ops.sps_amd.rope_qkv(q, k, v, freqs_cis, out_dtype)
     return tuple(t.transpose(1, 2) for t in outs)

@@ -1,7 +1,10 @@
 """Parity of the HIP attention kernels with the CPU oracle (GPU).
 
 Bar: masks bit-exact; bf16/f16 outputs and gradients within
-max-abs 2e-2 / rel 1e-2 of the float64 oracle evaluated on the same (16-bit) inputs.
+max-abs 2e-2 / rel 1e-2 of the float64 oracle evaluated on the same (16-bit) inputs. The one
+exception is the gradients at sharp-softmax inputs (activations x4 / x8, sm_scale = 1), where the
+reference's own 16-bit arithmetic misses that bound: there the kernels are held to the error of an
+emulation of that arithmetic (_scaled_check).
 """
 
 import math
@@ -335,19 +338,34 @@ def test_backward_reusing_forward_layout_is_identical(family):
         assert torch.equal(r, x) and torch.equal(r, y)
 
 
-# Activation scales seen in trained models: Q and K drawn with standard deviation 4 and 8, so the
-# scaled scores reach tens of units and the softmax is sharp. The kernels scale the fp32 scores
-# (S * sm_scale * log2 e, as triton_sps_flash_attention.py:78-79 does), so the forward keeps the
-# standard bound. The gradients go through bf16/f16-rounded P and dS, as the reference's own
-# kernels do (triton_sps_flash_attention.py:361-377); dQ and dK grow with the Q/K scale s and with
-# sm_scale, so their absolute bound is 2e-2 * s * max(1, |sm_scale| * sqrt(D)). With these inputs, an exact emulation of the reference's algorithm
-# (fp32 scores, 16-bit P and dS) measures up to 1.6x that bound on bf16 dK at s = 4 and 0.7x at
-# s = 8; the test allows 2.5x. Rounding a pre-scaled Q to bf16 instead (an earlier formulation of
-# these kernels) measures 5x in the forward and 17x on the gradients at s = 8.
-GRAD_FACTOR = 2.5
+# Activation scales seen in trained models: Q and K drawn with standard deviation 4 and 8, or
+# sm_scale = 1 at D = 64, so the scaled scores reach tens of units and the softmax is sharp. The
+# kernels scale the fp32 scores (S * sm_scale * log2 e, as triton_sps_flash_attention.py:78-79 does),
+# so the forward meets the plain bound against the exact (float64) oracle. The gradients go through
+# 16-bit P and dS, as the reference's own kernels do (:361-377, :471-488), and at these inputs that
+# arithmetic itself misses the plain bound on dQ and dK against the exact gradients (by 3-7x), and
+# two block sizes of the reference's autotuner disagree with each other beyond it
+# (tests/test_oracle_emulate.py, on oracle.emulate, the CPU emulation of the reference's
+# arithmetic). So each gradient is held to what the reference's arithmetic achieves on the same
+# inputs: with errors measured against the plain bound, the HIP gradient's worst element may not
+# exceed 1.5x the emulated reference's worst (the largest over its block sizes 32, 64, 128), nor its
+# root-mean-square error 1.25x the reference's.
+EMU_BLOCKS = (32, 64, 128)
+WORST_FACTOR, RMS_FACTOR = 1.5, 1.25
+
+
+def _bound_ratio(got, want):
+    err = (got.double() - want.double()).abs()
+    return float((err / (ATOL + RTOL * want.double().abs())).max())
+
+
+def _rms(got, want):
+    return float(((got.double() - want.double()) ** 2).mean().sqrt())
 
 
 def _scaled_check(family, n, d, s, dtype, window=64, sm_scale=None, seed=0):
+    from oracle import emulate as X
+
     dev = torch.device("cuda")
     b, h = 1, 2
     g = torch.Generator().manual_seed(seed)
@@ -364,14 +382,19 @@ def _scaled_check(family, n, d, s, dtype, window=64, sm_scale=None, seed=0):
     qn, kn, vn, don = (t.float().numpy() for t in (q, k, v, do))
     o_ref, _ = A.forward(qn, kn, vn, mask, scale)
     torch.testing.assert_close(out.float().cpu(), torch.from_numpy(o_ref).float(), atol=ATOL, rtol=RTOL)
-    dq, dk, dv = A.backward(qn, kn, vn, don, mask, scale)
-    for name, got, want, grows in (("dq", qg.grad, dq, True), ("dk", kg.grad, dk, True), ("dv", vg.grad, dv, False)):
-        want = torch.from_numpy(want)
-        err = (got.double().cpu() - want).abs()
-        grad_scale = s * max(1.0, abs(scale) * math.sqrt(d)) if grows else 1.0
-        bound = ATOL * grad_scale + RTOL * want.abs()
-        ratio = float((err / bound).max())
-        assert ratio <= GRAD_FACTOR, f"{name}: max error / bound = {ratio:.2f} (max abs error {float(err.max()):.4g})"
+    exact = [torch.from_numpy(x) for x in A.backward(qn, kn, vn, don, mask, scale)]
+    emulated = []
+    for bn in EMU_BLOCKS:
+        o_e, lse_e = X.forward(q, k, v, mask, scale, dtype=dtype, block_n=bn)
+        emulated.append(X.backward(q, k, v, o_e, lse_e, do, mask, scale, dtype=dtype))
+    for i, (name, got) in enumerate((("dq", qg.grad), ("dk", kg.grad), ("dv", vg.grad))):
+        got = got.cpu()
+        worst = _bound_ratio(got, exact[i])
+        worst_ref = max(_bound_ratio(e[i], exact[i]) for e in emulated)
+        rms, rms_ref = _rms(got, exact[i]), sum(_rms(e[i], exact[i]) for e in emulated) / len(emulated)
+        assert worst <= max(1.0, WORST_FACTOR * worst_ref), (
+            f"{name}: worst error / plain bound {worst:.2f}, the reference's arithmetic {worst_ref:.2f}")
+        assert rms <= RMS_FACTOR * rms_ref + 1e-7, f"{name}: rms error {rms:.3g}, the reference's arithmetic {rms_ref:.3g}"
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
@@ -384,8 +407,8 @@ def test_scaled_activations(family, s, dtype):
 @pytest.mark.parametrize("sm_scale", [-0.125, 0.0, 1.0])
 @pytest.mark.parametrize("family", ["sps", "reverse_sps", "full"])
 def test_any_sm_scale(family, sm_scale):
-    # The reference takes any sm_scale (it multiplies the fp32 scores by it); masks are applied to the
-    # scaled scores, so a zero scale gives the mean of the visible values and a negative one flips
+    # The reference takes any sm_scale (it multiplies the fp32 scores by it and adds its masks to
+    # the scaled scores): a zero scale gives the mean of the visible values, a negative one flips
     # the scores.
     _scaled_check(family, 256, 64, 1.0, torch.bfloat16, window=5, sm_scale=sm_scale, seed=3)
 
@@ -401,3 +424,20 @@ def test_c1_shape_forward_against_oracle():
     mask = M.batch_mask(N.FAMILY_SPS, None, n=C1.n, window=C1.window, batch=C1.batch)
     o_ref, _ = A.forward(q.float().numpy(), k.float().numpy(), v.float().numpy(), mask, 1 / math.sqrt(C1.head_dim))
     torch.testing.assert_close(out.float().cpu(), torch.from_numpy(o_ref).float(), atol=ATOL, rtol=RTOL)
+
+
+def test_second_backward_over_a_retained_graph():
+    # The reference's autograd.Function allows backward(retain_graph=True) twice; the saved layout
+    # workspace is not declared mutated by the backward, so the second pass is accepted and gives the
+    # same gradients.
+    rng = np.random.default_rng(2)
+    b, h, n, d = 1, 2, 512, 64
+    docs = torch.tensor(_packed_docs(rng, b, n // 2, "sps", max_len=100), device="cuda")
+    g = torch.Generator().manual_seed(2)
+    q, k, v, do = (torch.randn((b, h, n, d), generator=g).to(torch.bfloat16).cuda() for _ in range(4))
+    qg, kg, vg = (t.requires_grad_(True) for t in (q, k, v))
+    out = SA.sps_sliding_attention(qg, kg, vg, 0.125, 16, documents_idx_BxT=docs)
+    first = torch.autograd.grad(out, (qg, kg, vg), do, retain_graph=True)
+    second = torch.autograd.grad(out, (qg, kg, vg), do)
+    for x, y in zip(first, second):
+        assert torch.equal(x, y)

@@ -49,3 +49,62 @@ def test_compiled_inference_without_grad():
     compiled = torch.compile(lambda x: sps_amd.full_attention(x, x, x, 0.125), fullgraph=True, backend="aot_eager")
     with torch.no_grad():
         assert torch.equal(compiled(q), eager)
+
+
+def _reference_apply_rotary_emb(xq, xk, freqs_cis):
+    # The reference's own formula (model.py:201-230), as the CPU original the installed dispatcher
+    # wraps: fp32 complex product, results in the inputs' dtype.
+    xq_ = torch.view_as_complex(xq.float().reshape(*xq.shape[:-1], -1, 2))
+    xk_ = torch.view_as_complex(xk.float().reshape(*xk.shape[:-1], -1, 2))
+    f = freqs_cis.view(1, xq_.shape[1], 1, xq_.shape[-1])
+    return torch.view_as_real(xq_ * f).flatten(3).type_as(xq), torch.view_as_real(xk_ * f).flatten(3).type_as(xk)
+
+
+def test_compiled_block_through_the_installed_rope_matches_eager(monkeypatch):
+    # The SPS attention module's forward (sps/core.py:45-80) under torch.compile(fullgraph=True): QKV
+    # projection, apply_rotary_emb looked up in modeling.models.model at call time (:50-52) after
+    # install_into_modeling() made it the device dispatcher (CUDA tensors -> the HIP RoPE custom op),
+    # bf16 casts, sps_sliding_attention, output projection. Output and the projections' gradients
+    # equal eager.
+    import sys
+    import types
+
+    model_mod = types.ModuleType("modeling.models.model")
+    model_mod.apply_rotary_emb = _reference_apply_rotary_emb
+    monkeypatch.setitem(sys.modules, "modeling.models.model", model_mod)
+    sps_amd.install_into_modeling()
+    assert model_mod.apply_rotary_emb.__sps_amd_original__ is _reference_apply_rotary_emb
+    torch._dynamo.reset()
+
+    b, two_t, h, d, w = 2, 256, 4, 64, 16
+    c = h * d
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn((b, two_t, c), generator=g).cuda()
+    inv = 1.0 / (10000.0 ** (torch.arange(0, d, 2).float() / d))
+    freqs = torch.polar(torch.ones(two_t, d // 2), torch.outer(torch.arange(two_t).float(), inv)).cuda()
+    docs = torch.tensor(np.repeat(np.array([[0] * 50 + [1] * 78] * b), 2, axis=1), device="cuda")
+    torch.manual_seed(0)
+    c_attn, c_proj = torch.nn.Linear(c, 3 * c).cuda(), torch.nn.Linear(c, c).cuda()
+
+    def block(x):
+        from modeling.models.model import apply_rotary_emb
+
+        q, k, v = c_attn(x).split(c, dim=2)
+        q, k = q.view(b, two_t, h, d), k.view(b, two_t, h, d)
+        v = v.view(b, two_t, h, d).transpose(1, 2)
+        q, k = apply_rotary_emb(q, k, freqs_cis=freqs)
+        q, k, v = q.transpose(1, 2).to(torch.bfloat16), k.transpose(1, 2).to(torch.bfloat16), v.to(torch.bfloat16)
+        y = sps_amd.sps_sliding_attention(q, k, v, 1 / math.sqrt(d), w, documents_idx_BxT=docs)
+        y = y.transpose(1, 2).contiguous().view(b, two_t, c).to(c_proj.weight.dtype)
+        return c_proj(y).square().mean()
+
+    results = []
+    for fn in (block, torch.compile(block, fullgraph=True, backend="aot_eager")):
+        for p in (*c_attn.parameters(), *c_proj.parameters()):
+            p.grad = None
+        loss = fn(x)
+        loss.backward()
+        torch.cuda.synchronize()
+        results.append([loss.detach()] + [p.grad.clone() for p in (*c_attn.parameters(), *c_proj.parameters())])
+    for got, want in zip(results[1], results[0]):
+        torch.testing.assert_close(got, want, atol=0, rtol=0)

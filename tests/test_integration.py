@@ -45,6 +45,9 @@ def _install_stand_ins(monkeypatch):
     for consumer in ("modeling.models.full_attention_model", "modeling.models.reverse_sps.core"):
         mods[consumer].generate_left_padded_document_idx = \
             mods["modeling.models.model"].generate_left_padded_document_idx
+    for consumer in ("modeling.models.full_attention_model", "modeling.models.reverse_sps.core",
+                     "modeling.models.reverse_sps.inference"):
+        mods[consumer].apply_rotary_emb = mods["modeling.models.model"].apply_rotary_emb
     for n, m in mods.items():
         monkeypatch.setitem(sys.modules, n, m)
     for n in ["modeling.models.attention.triton_sps_flash_attention",
@@ -98,9 +101,15 @@ def test_cpu_calls_keep_the_reference_path_and_cuda_calls_reach_the_kernels(monk
         assert fn(cpu, [], attn_dtype=torch.float32) == "masked_kv_attention"
         assert fn(q_BxHxD=cpu, segments=[], attn_dtype=torch.float32) == "masked_kv_attention"
         assert fn(_CudaLike(), [], attn_dtype=torch.bfloat16) == "gpu"
-    rope = mods["modeling.models.model"].apply_rotary_emb
-    assert rope(cpu, cpu, cpu) == "apply_rotary_emb"
-    assert rope(_CudaLike(), None, None) == "gpu"
+    # apply_rotary_emb: where it is defined, and in the three modules that import it by name
+    # (full_attention_model.py:26-32, reverse_sps/core.py:16-19, reverse_sps/inference.py:13-14).
+    for consumer in ("modeling.models.model", "modeling.models.full_attention_model",
+                     "modeling.models.reverse_sps.core", "modeling.models.reverse_sps.inference"):
+        rope = mods[consumer].apply_rotary_emb
+        assert rope(cpu, cpu, cpu) == "apply_rotary_emb"
+        assert rope(_CudaLike(), None, None) == "gpu"
+        assert rope(xq=_CudaLike(), xk=None, freqs_cis=None) == "gpu"
+    assert gpu_calls.count("apply_rotary_emb") == 8
     for consumer in ("modeling.models.model", "modeling.models.full_attention_model",
                      "modeling.models.reverse_sps.core"):
         ids = mods[consumer].generate_left_padded_document_idx

@@ -65,6 +65,10 @@ def _fwd(**over):
         (dict(strides=(64 * 64, 64 * 64, 60)), N.SPS_E_INVALID, "multiple of 8"),
         (dict(docs=0x30000, docs_dtype=N.DTYPE_F32), N.SPS_E_INVALID, "int32 or int64"),
         (dict(docs=0x30000, docs_dtype=N.DTYPE_I64, ws_bytes=0), N.SPS_E_WORKSPACE, "workspace"),
+        # any finite scale is taken (zero and negative ones included); NaN and infinities are not
+        (dict(sm_scale=float("nan")), N.SPS_E_INVALID, "sm_scale"),
+        (dict(sm_scale=float("inf")), N.SPS_E_INVALID, "sm_scale"),
+        (dict(sm_scale=float("-inf")), N.SPS_E_INVALID, "sm_scale"),
     ],
 )
 @cpu_only
@@ -124,6 +128,11 @@ def test_backward_pass_selector_validation():
                                    p, st, p, st, p, st, None, N.DTYPE_I64, 0, 0.125, 4, 0, -1, None, 0, None)
         assert rc == N.SPS_E_INVALID, bad
         assert "pass selector" in N.last_error()
+    for bad_scale in (float("nan"), float("inf")):
+        rc = lib.sps_attn_bwd_pass(N.BWD_DQ | N.BWD_DKDV, 1, 1, 1, 64, 64, N.DTYPE_BF16, p, st, p, st, p, st, p, st,
+                                   p, st, 0x20000, p, st, p, st, p, st, None, N.DTYPE_I64, 0, bad_scale, 4, 0, -1,
+                                   0x50000, 0x40000, None)
+        assert rc == N.SPS_E_INVALID and "sm_scale" in N.last_error()
 
 
 def _kv_update(window=2, ring_storage=4, kv_dtype=N.DTYPE_BF16, new_dtype=N.DTYPE_BF16, len_dtype=N.DTYPE_I64,
