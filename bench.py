@@ -595,6 +595,23 @@ def bench_decode(cfg, steps: int, warmup: int):
 
     u_us = timed(update_call, reps=3)
     upd_ret_len.zero_()
+
+    # The whole decode step of the layer: the attention, then the update. Two launches and then the
+    # update's own (decode, then sps_kv_update), against the update folded into the attention's
+    # launches (sps_decode_kv_update). The update writes caches of the C5 shape of its own, as above,
+    # so every timed step reads the same C5 lengths; the GPU tests run the fused step on the
+    # segments' own caches.
+    def step_separate():
+        kernel_call()
+        run_kv_update(upd_args)
+
+    def step_fused():
+        DA._run_decode(q4, 1, segs, ex, [1, 1], out, kv_update=upd_args)
+
+    sep_us = timed(step_separate)
+    upd_ret_len.zero_()
+    fused_us = timed(step_fused)
+    upd_ret_len.zero_()
     upd_bytes = 8 * B * H * D * 2  # four [B, H, D] bf16 rows read and written once
     nbytes = decode_bytes(cfg, lengths, nq=1, n_extra=2, kv_bytes=2)
     k_med = statistics.median(k_us)
@@ -611,6 +628,11 @@ def bench_decode(cfg, steps: int, warmup: int):
         "q2_algorithmic_bytes": q2_bytes,
         "kv_update_us": round(statistics.median(u_us), 3),
         "kv_update_gbps": round(upd_bytes / (statistics.median(u_us) * 1e-6) / 1e9, 1),
+        "step_with_kv_update_us": {"fused": round(statistics.median(fused_us), 3),
+                                   "separate": round(statistics.median(sep_us), 3),
+                                   "note": "the decode step of one layer including its KV update: folded into "
+                                           "the attention's launches (sps_decode_kv_update) against the "
+                                           "attention followed by the update's own launch"},
         "gbps": round(gbps, 1),
         "algorithmic_bytes": nbytes,
         "roofline": {"kernel": "decode_partial_kernel + decode_merge_kernel", "bound": "hbm",
@@ -619,10 +641,6 @@ def bench_decode(cfg, steps: int, warmup: int):
                      "traffic": (lambda t: t["decode_partial_kernel"] + t["decode_merge_kernel"]
                                  if "decode_partial_kernel" in t and "decode_merge_kernel" in t else None)(
                                      recorded_traffic())},
-        "kv_update_note": "a launch of its own after the attention (as fused_sps_kv_update is in the reference): "
-                          "the merge kernel reads the ring and retained lengths the update advances, and the "
-                          "ring length is shared by all heads of a sequence, so a fused update would need a "
-                          "grid-wide ordering between the last reader and the writer of each sequence",
         "_api_wall_s": time.perf_counter() - t0,
     }
 
@@ -724,7 +742,9 @@ def main() -> int:
         log(f"C5 decode: {args.decode_steps} timed steps")
         dec = bench_decode(C5, args.decode_steps, 20)
         dec.pop("_api_wall_s")
-        log(f"C5: {dec['us_per_step']} us/step, {dec['gbps']} GB/s")
+        log(f"C5: {dec['us_per_step']} us/step, {dec['gbps']} GB/s; with the KV update "
+            f"{dec['step_with_kv_update_us']['fused']} us fused, {dec['step_with_kv_update_us']['separate']} us "
+            f"as two calls (update alone {dec['kv_update_us']} us)")
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline (C3 sample)")

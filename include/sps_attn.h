@@ -24,6 +24,8 @@
  *   sps_decode                    <- triton_segmented_q1_attention (utils/decode_attention.py:393-480),
  *                                    triton_segmented_q2_attention (utils/decode_attention.py:483-594)
  *   sps_kv_update                 <- fused_sps_kv_update (utils/decode_attention_fast.py:139-221)
+ *   sps_decode_kv_update          <- the decode step's attention over the caches followed by
+ *                                    fused_sps_kv_update (reverse_sps/inference.py:169-238, 322-362)
  *   sps_rope_qkv                  <- apply_rotary_emb (model.py:201-230) + the transposes and casts
  *                                    before the attention call (sps/core.py:45-55)
  *   sps_prefill_to_decode         <- _materialize_prefill_layer_state
@@ -236,6 +238,42 @@ int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v,
                   const void* k_window, const void* v_window, const void* k_retained, const void* v_retained,
                   const int64_t* new_strides, const void* active, int active_dtype, int64_t active_stride,
                   void* stream);
+
+/* Workspace needed by sps_decode_kv_update: sps_decode's partial records plus a length snapshot. */
+size_t sps_decode_kv_update_workspace_bytes(int B, int H, int D, int nq, int kv_dtype, int n_seg,
+                                            const int64_t* seg_scan);
+
+/*
+ * One decode step of one layer: sps_decode, then sps_kv_update, as one entry point with the update
+ * folded into the attention's launches (replaces the reference's decode step pair, the segmented
+ * attention over the caches followed by fused_sps_kv_update: reverse_sps/inference.py:322-362 with
+ * :169-238, utils/decode_attention_fast.py:139-221). The attention reads the caches as they were
+ * before the update. Arguments: sps_decode's from B to out_strides, then sps_kv_update's from
+ * ring_k to active_stride (the caches in kv_dtype, the decode's K/V dtype), then the workspace
+ * (sps_decode_kv_update_workspace_bytes) and the stream. When the update copies new rows of the
+ * cache dtype with 16-byte aligned rows and strides (and the segments hold at least one chunk), it
+ * runs inside the attention's merge launch: the partial kernel snapshots the lengths, and the merge
+ * writes the rows and advances the lengths from the snapshot; otherwise the update is a launch of
+ * its own after the attention. Results are those of the two calls in that order.
+ */
+int sps_decode_kv_update(int B, int H, int D, int nq,
+                         const void* q, int q_dtype, const int64_t* q_strides,
+                         int kv_dtype, int n_seg,
+                         const void* const* seg_k, const int64_t* seg_k_strides,
+                         const void* const* seg_v, const int64_t* seg_v_strides,
+                         const void* const* seg_len, const int* seg_len_dtype, const int* seg_len_per_head,
+                         const int64_t* seg_scan,
+                         int n_extra, const void* const* extra_k, const void* const* extra_v, int extra_dtype,
+                         const int64_t* extra_strides, const int* extra_query_mask,
+                         float sm_scale, float* out, const int64_t* out_strides,
+                         void* ring_k, void* ring_v, const int64_t* ring_strides, int ring_storage,
+                         int window_tokens, void* ring_len, void* ring_pos, const int64_t* ring_len_strides,
+                         void* ret_k, void* ret_v, const int64_t* ret_strides, int ret_storage, void* ret_len,
+                         const int64_t* ret_len_strides, int len_dtype, int new_dtype,
+                         const void* k_window, const void* v_window, const void* k_retained,
+                         const void* v_retained, const int64_t* new_strides,
+                         const void* active, int active_dtype, int64_t active_stride,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Pre-attention rotary embedding and cast, one pass (replaces apply_rotary_emb, model.py:201-230,

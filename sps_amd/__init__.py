@@ -3,7 +3,9 @@
 Drop-in replacements for the reference's attention entry points:
   prefill / training: ``sps_sliding_attention``, ``reverse_sps_sliding_attention``, ``full_attention``
   decode:             ``KVSegment``, ``triton_segmented_q1_attention``, ``triton_segmented_q2_attention``,
-                      ``masked_kv_attention``, ``fused_sps_kv_update`` (KV-cache update)
+                      ``masked_kv_attention``, ``fused_sps_kv_update`` (KV-cache update),
+                      ``segmented_q{1,2}_attention_with_kv_update`` (a decode step's attention and
+                      KV update in the attention's launches)
   pre-attention:      ``apply_rotary_emb``, ``rope_qkv_for_attention`` (RoPE + casts + layout, one launch)
   prefill -> decode:  ``prefill_to_decode``, ``materialize_prefill_layer_state`` (decode caches, one launch)
   document ids:       ``document_ids`` (EOS / left-pad rules, interleaved for the SPS families)
@@ -17,7 +19,11 @@ from .decode_attention import (
     triton_segmented_q1_attention,
     triton_segmented_q2_attention,
 )
-from .decode_attention_fast import fused_sps_kv_update
+from .decode_attention_fast import (
+    fused_sps_kv_update,
+    segmented_q1_attention_with_kv_update,
+    segmented_q2_attention_with_kv_update,
+)
 from .doc_ids import document_ids, left_padded_document_ids
 from .integration import install_into_modeling
 from .rope import apply_rotary_emb, rope_qkv_for_attention
@@ -32,6 +38,8 @@ __all__ = [
     "triton_segmented_q2_attention",
     "masked_kv_attention",
     "fused_sps_kv_update",
+    "segmented_q1_attention_with_kv_update",
+    "segmented_q2_attention_with_kv_update",
     "document_ids",
     "left_padded_document_ids",
     "install_into_modeling",

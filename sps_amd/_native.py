@@ -44,6 +44,8 @@ EXPORTED_SYMBOLS = (
     "sps_decode",
     "sps_decode_static",
     "sps_kv_update",
+    "sps_decode_kv_update_workspace_bytes",
+    "sps_decode_kv_update",
     "sps_rope_qkv",
     "sps_prefill_to_decode",
     "sps_document_ids",
@@ -116,6 +118,19 @@ _SIGNATURES = {
         + [_p, _p, _pi64, _i32, _p, _pi64, _i32]  # retained, length dtype
         + [_i32, _p, _p, _p, _p, _pi64]  # new K/V
         + [_p, _i32, _i64, _p],
+    ),
+    "sps_decode_kv_update_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _pi64]),
+    "sps_decode_kv_update": (
+        _i32,
+        [_i32, _i32, _i32, _i32, _p, _i32, _pi64, _i32, _i32]
+        + [C.POINTER(_p), _pi64, C.POINTER(_p), _pi64, C.POINTER(_p), _pi32, _pi32, _pi64]
+        + [_i32, C.POINTER(_p), C.POINTER(_p), _i32, _pi64, _pi32]
+        + [_f32, _p, _pi64]
+        + [_p, _p, _pi64, _i32, _i32, _p, _p, _pi64]  # ring
+        + [_p, _p, _pi64, _i32, _p, _pi64, _i32]  # retained, length dtype
+        + [_i32, _p, _p, _p, _p, _pi64]  # new K/V
+        + [_p, _i32, _i64]  # active
+        + [_p, _sz, _p],
     ),
     "sps_rope_qkv": (
         _i32,

@@ -314,6 +314,11 @@ size_t sps_decode_workspace_bytes(int B, int H, int D, int nq, int kv_dtype, int
 
 }  // extern "C"
 
+// Bytes of the length snapshot of sps_decode_kv_update (after the partial records, 256-byte aligned).
+static size_t decode_snapshot_bytes(int B, int H) {
+  return align_up((size_t)B * H * sps::kSnapWords * sizeof(int64_t));
+}
+
 // Validation and launch shared by sps_decode (caller's workspace) and sps_decode_static (the
 // library's scratch array). `workspace` is only read after `workspace_bytes` has been checked.
 static int decode_impl(int B, int H, int D, int nq, const void* q, int q_dtype, const int64_t* q_strides,
@@ -322,7 +327,8 @@ static int decode_impl(int B, int H, int D, int nq, const void* q, int q_dtype, 
                        const int* seg_len_dtype, const int* seg_len_per_head, const int64_t* seg_scan, int n_extra,
                        const void* const* extra_k, const void* const* extra_v, int extra_dtype,
                        const int64_t* extra_strides, const int* extra_query_mask, float sm_scale, float* out,
-                       const int64_t* out_strides, void* workspace, size_t workspace_bytes, void* stream) {
+                       const int64_t* out_strides, void* workspace, size_t workspace_bytes, void* stream,
+                       const sps::KvUpdateArgs* upd = nullptr) {
   if (B < 0 || H < 0) return fail(SPS_E_INVALID, "negative size B=%d H=%d", B, H);
   if (nq != 1 && nq != 2) return fail(SPS_E_INVALID, "nq must be 1 or 2 (got %d)", nq);
   if (!decode_head_dim(D)) return fail(SPS_E_UNSUPPORTED, "decode head_dim %d not supported", D);
@@ -339,7 +345,8 @@ static int decode_impl(int B, int H, int D, int nq, const void* q, int q_dtype, 
   if ((int64_t)B * H == 0) return SPS_OK;
   if (!q || !q_strides || !out || !out_strides) return fail(SPS_E_INVALID, "q/out: null pointer");
   if (!(std::isfinite(sm_scale))) return fail(SPS_E_INVALID, "sm_scale must be finite");
-  const size_t need = sps_decode_workspace_bytes(B, H, D, nq, kv_dtype, n_seg, seg_scan);
+  const size_t part_bytes = sps_decode_workspace_bytes(B, H, D, nq, kv_dtype, n_seg, seg_scan);
+  const size_t need = part_bytes + (upd ? decode_snapshot_bytes(B, H) : 0);
   if (workspace_bytes < need) return fail(SPS_E_WORKSPACE, "workspace too small: %zu < %zu", workspace_bytes, need);
   sps::DecodeArgs a;
   std::memset(&a, 0, sizeof(a));
@@ -414,7 +421,19 @@ static int decode_impl(int B, int H, int D, int nq, const void* q, int q_dtype, 
   a.o_sh = out_strides[2];
   a.scale2 = sm_scale * 1.4426950408889634f;
   a.part = static_cast<float*>(workspace);
-  return hip_status(sps::launch_decode(a, D, kv_dtype, static_cast<hipStream_t>(stream)), "decode");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!upd) return hip_status(sps::launch_decode(a, D, kv_dtype, st), "decode");
+  // The update folds into the launch when it copies 16-byte pieces (no dtype conversion, aligned rows)
+  // and the grid has a first chunk for every (sequence, head) to take the length snapshot; otherwise
+  // it runs as its own launch after the attention (same results).
+  if (upd->vec16 && a.n_chunks > 0) {
+    a.snap = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + part_bytes);
+    a.upd = *upd;
+    return hip_status(sps::launch_decode(a, D, kv_dtype, st), "decode with kv update");
+  }
+  const int rc = hip_status(sps::launch_decode(a, D, kv_dtype, st), "decode");
+  if (rc) return rc;
+  return hip_status(sps::launch_kv_update(*upd, st), "kv update");
 }
 
 // Scratch of sps_decode_static: the per-chunk partial records live in this array instead of a
@@ -492,14 +511,19 @@ int sps_decode_static(int B, int H, int D, int nq, const void* q, int q_dtype, c
                      kDecodeScratchBytes, stream);
 }
 
-int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v, const int64_t* ring_strides,
-                  int ring_storage, int window_tokens, void* ring_len, void* ring_pos,
-                  const int64_t* ring_len_strides, void* ret_k, void* ret_v, const int64_t* ret_strides,
-                  int ret_storage, void* ret_len, const int64_t* ret_len_strides, int len_dtype, int new_dtype,
-                  const void* k_window, const void* v_window, const void* k_retained, const void* v_retained,
-                  const int64_t* new_strides, const void* active, int active_dtype, int64_t active_stride,
-                  void* stream) {
-  g_last_error.clear();
+}  // extern "C"
+
+// Validates the arguments of a KV-cache update and fills its argument block (shared by
+// sps_kv_update and sps_decode_kv_update). Returns SPS_OK, or an error with nothing launched; *empty
+// is set when there is nothing to do (B * H * D == 0).
+static int kv_update_setup(sps::KvUpdateArgs& a, bool* empty, int B, int H, int D, int kv_dtype, void* ring_k,
+                           void* ring_v, const int64_t* ring_strides, int ring_storage, int window_tokens,
+                           void* ring_len, void* ring_pos, const int64_t* ring_len_strides, void* ret_k, void* ret_v,
+                           const int64_t* ret_strides, int ret_storage, void* ret_len,
+                           const int64_t* ret_len_strides, int len_dtype, int new_dtype, const void* k_window,
+                           const void* v_window, const void* k_retained, const void* v_retained,
+                           const int64_t* new_strides, const void* active, int active_dtype, int64_t active_stride) {
+  *empty = false;
   if (B < 0 || H < 0 || D < 0) return fail(SPS_E_INVALID, "negative size B=%d H=%d D=%d", B, H, D);
   auto float_type = [](int t) { return t == SPS_DTYPE_BF16 || t == SPS_DTYPE_F16 || t == SPS_DTYPE_F32; };
   if (!float_type(kv_dtype)) return fail(SPS_E_UNSUPPORTED, "cache dtype code %d not supported", kv_dtype);
@@ -512,7 +536,10 @@ int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v,
   else if (active_dtype == SPS_DTYPE_I64) active_bytes = 8;
   else return fail(SPS_E_INVALID, "active mask must be bool/uint8, int32 or int64 (dtype code %d)", active_dtype);
   if (ret_storage < 0 || ring_storage < 0) return fail(SPS_E_INVALID, "negative cache storage");
-  if ((int64_t)B * H * D == 0) return SPS_OK;
+  if ((int64_t)B * H * D == 0) {
+    *empty = true;
+    return SPS_OK;
+  }
   if (!active || !ret_k || !ret_v || !ret_len || !k_retained || !v_retained || !ret_strides || !ret_len_strides ||
       !new_strides)
     return fail(SPS_E_INVALID, "retained cache / new K/V / active mask: null pointer");
@@ -522,7 +549,6 @@ int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v,
     if (window_tokens > ring_storage)
       return fail(SPS_E_INVALID, "window_tokens %d exceeds the ring storage %d", window_tokens, ring_storage);
   }
-  sps::KvUpdateArgs a;
   std::memset(&a, 0, sizeof(a));
   a.B = B;
   a.H = H;
@@ -585,7 +611,62 @@ int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v,
                              a.vw_sb, a.vw_sh};
   for (int64_t st : strides) vec = vec && (st * esz) % 16 == 0;
   a.vec16 = vec ? 1 : 0;
+  return SPS_OK;
+}
+
+
+extern "C" {
+
+int sps_kv_update(int B, int H, int D, int kv_dtype, void* ring_k, void* ring_v, const int64_t* ring_strides,
+                  int ring_storage, int window_tokens, void* ring_len, void* ring_pos,
+                  const int64_t* ring_len_strides, void* ret_k, void* ret_v, const int64_t* ret_strides,
+                  int ret_storage, void* ret_len, const int64_t* ret_len_strides, int len_dtype, int new_dtype,
+                  const void* k_window, const void* v_window, const void* k_retained, const void* v_retained,
+                  const int64_t* new_strides, const void* active, int active_dtype, int64_t active_stride,
+                  void* stream) {
+  g_last_error.clear();
+  sps::KvUpdateArgs a;
+  bool empty = false;
+  const int rc = kv_update_setup(a, &empty, B, H, D, kv_dtype, ring_k, ring_v, ring_strides, ring_storage,
+                                 window_tokens, ring_len, ring_pos, ring_len_strides, ret_k, ret_v, ret_strides,
+                                 ret_storage, ret_len, ret_len_strides, len_dtype, new_dtype, k_window, v_window,
+                                 k_retained, v_retained, new_strides, active, active_dtype, active_stride);
+  if (rc || empty) return rc;
   return hip_status(sps::launch_kv_update(a, static_cast<hipStream_t>(stream)), "kv update");
+}
+
+size_t sps_decode_kv_update_workspace_bytes(int B, int H, int D, int nq, int kv_dtype, int n_seg,
+                                            const int64_t* seg_scan) {
+  if (!decode_head_dim(D) || B < 0 || H < 0 || n_seg < 0 || n_seg > sps::kMaxDecodeSegs) return 0;
+  return sps_decode_workspace_bytes(B, H, D, nq, kv_dtype, n_seg, seg_scan) + decode_snapshot_bytes(B, H);
+}
+
+int sps_decode_kv_update(int B, int H, int D, int nq, const void* q, int q_dtype, const int64_t* q_strides,
+                         int kv_dtype, int n_seg, const void* const* seg_k, const int64_t* seg_k_strides,
+                         const void* const* seg_v, const int64_t* seg_v_strides, const void* const* seg_len,
+                         const int* seg_len_dtype, const int* seg_len_per_head, const int64_t* seg_scan,
+                         int n_extra, const void* const* extra_k, const void* const* extra_v, int extra_dtype,
+                         const int64_t* extra_strides, const int* extra_query_mask, float sm_scale, float* out,
+                         const int64_t* out_strides, void* ring_k, void* ring_v, const int64_t* ring_strides,
+                         int ring_storage, int window_tokens, void* ring_len, void* ring_pos,
+                         const int64_t* ring_len_strides, void* ret_k, void* ret_v, const int64_t* ret_strides,
+                         int ret_storage, void* ret_len, const int64_t* ret_len_strides, int len_dtype,
+                         int new_dtype, const void* k_window, const void* v_window, const void* k_retained,
+                         const void* v_retained, const int64_t* new_strides, const void* active, int active_dtype,
+                         int64_t active_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  sps::KvUpdateArgs u;
+  bool empty = false;
+  int rc = kv_update_setup(u, &empty, B, H, D, kv_dtype, ring_k, ring_v, ring_strides, ring_storage, window_tokens,
+                           ring_len, ring_pos, ring_len_strides, ret_k, ret_v, ret_strides, ret_storage, ret_len,
+                           ret_len_strides, len_dtype, new_dtype, k_window, v_window, k_retained, v_retained,
+                           new_strides, active, active_dtype, active_stride);
+  if (rc) return rc;
+  if (n_seg > 0 && !seg_scan) return fail(SPS_E_INVALID, "seg_scan: null pointer");
+  return decode_impl(B, H, D, nq, q, q_dtype, q_strides, kv_dtype, n_seg, seg_k, seg_k_strides, seg_v,
+                     seg_v_strides, seg_len, seg_len_dtype, seg_len_per_head, seg_scan, n_extra, extra_k, extra_v,
+                     extra_dtype, extra_strides, extra_query_mask, sm_scale, out, out_strides, workspace,
+                     workspace_bytes, stream, empty ? nullptr : &u);
 }
 
 int sps_rope_qkv(int B, int N, int H, int D, int in_dtype, const void* q, const int64_t* q_strides, const void* k,

@@ -18,6 +18,15 @@
 // length exit before touching K/V. A second small kernel merges the partials with the extras: one
 // wave per (sequence, head, query slot), lanes over chunks for the max and the sums, then batched
 // coalesced reads of the accumulators (no chain of dependent loads per chunk).
+//
+// KV update in the same launch (sps_decode_kv_update; reference decode step: the attention over the
+// caches, then fused_sps_kv_update, reverse_sps/inference.py:169-238, 437-470). The update writes the
+// rows and lengths the attention reads, so the two must not overlap: the partial kernel reads every
+// cache row before the merge kernel starts (stream order), and the first-chunk workgroup of each
+// (sequence, head), which the grid always launches, stores the old lengths in a snapshot. The merge
+// kernel reads only the snapshot: its query-0 wave of each (sequence, head) writes that head's new
+// ring and retained rows and advances its retained length; the wave of head 0 advances the ring's
+// length or position. No wave of the launch reads a length another one writes.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -130,6 +139,18 @@ __device__ __forceinline__ float dot8_packed(u32x4_t k, u32x4_t q, float acc) {
   return acc;
 }
 
+// The lengths the merge kernel and the folded KV update use, as they are before the update (one
+// thread of the (b, h)'s first-chunk workgroup).
+__device__ __forceinline__ void snapshot_lengths(const DecodeArgs& a, int b, int h) {
+  int64_t* sn = a.snap + ((int64_t)b * a.H + h) * kSnapWords;
+  for (int s = 0; s < a.n_seg; ++s) sn[s] = seg_live_len(a.seg[s], b, h, a.H);
+  const KvUpdateArgs& u = a.upd;
+  sn[kSnapRingLen] = u.window > 0 ? cache_len_load(u.ring_len, (int64_t)b * u.ring_len_sb, u.len_i64) : 0;
+  sn[kSnapRingPos] = u.window > 0 ? cache_len_load(u.ring_pos, (int64_t)b * u.ring_pos_sb, u.len_i64) : 0;
+  sn[kSnapRetLen] = cache_len_load(u.ret_len, b * u.ret_len_sb + h * u.ret_len_sh, u.len_i64);
+  sn[kSnapActive] = cache_flag_load(u.active, (int64_t)b * u.active_sb, u.active_bytes);
+}
+
 // PQ: the query is in the K/V's 16-bit type with 16-byte aligned rows (the host checks), so the
 // scores are packed dot products of raw K words and raw query words, with no conversion of K.
 // Three waves per SIMD: the two-query form otherwise compiles to 170 VGPRs, one wave per SIMD fewer
@@ -149,6 +170,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 16 ? 1
   __shared__ __attribute__((aligned(16))) float s_acc[4][NQ][D];
 
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  if (a.snap && c == 0 && threadIdx.x == 0) snapshot_lengths(a, b, h);
   int si = 0;
   while (si + 1 < a.n_seg && c >= a.seg[si + 1].chunk_base) ++si;
   const DecodeSeg sg = a.seg[si];
@@ -301,10 +323,34 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
   constexpr int DPL = (D + 63) / 64;  // output elements per lane
   constexpr int REC = DecodeGeom<D, 2>::REC;
   const int qi = blockIdx.x, h = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+  // With the KV update folded in, lengths come from the snapshot only (this launch writes them).
+  const int64_t* snap = a.snap ? a.snap + ((int64_t)b * a.H + h) * kSnapWords : nullptr;
+  const bool upd = snap && qi == 0;
+  // The update's new rows, 16-byte pieces numbered (row r in {ring K, ring V, retained K, retained
+  // V}, piece j), loaded first: nothing else depends on them, and they are stored at the end.
+  constexpr int kUpdPieces = 4;  // per lane: 4 rows of at most 1 KiB (D = 256 in fp32)
+  u32x4_t uval[kUpdPieces];
+  int upr = 0;
+  if (upd) {
+    const KvUpdateArgs& u = a.upd;
+    upr = u.D * (u.kv_dtype == 2 ? 4 : 2) / 16;
+#pragma unroll
+    for (int i = 0; i < kUpdPieces; ++i) {
+      const int pc = lane + 64 * i, r = pc / upr, j = pc - r * upr;
+      if (r < 4 && (r >= 2 || u.window > 0)) {
+        const void* src = r == 0 ? u.kw : r == 1 ? u.vw : r == 2 ? u.kr : u.vr;
+        const int64_t sb = r == 0 ? u.kw_sb : r == 1 ? u.vw_sb : r == 2 ? u.kr_sb : u.vr_sb;
+        const int64_t sh = r == 0 ? u.kw_sh : r == 1 ? u.vw_sh : r == 2 ? u.kr_sh : u.vr_sh;
+        const int esz = u.kv_dtype == 2 ? 4 : 2;
+        uval[i] = *reinterpret_cast<const u32x4_t*>(static_cast<const char*>(src) + (b * sb + h * sh) * esz + j * 16);
+      }
+    }
+  }
   int nc[kMaxDecodeSegs] = {0, 0, 0};
   int total = 0;
   for (int s = 0; s < a.n_seg; ++s) {
-    nc[s] = (seg_live_len(a.seg[s], b, h, a.H) + a.chunk_keys - 1) / a.chunk_keys;
+    const int live = snap ? (int)snap[s] : seg_live_len(a.seg[s], b, h, a.H);
+    nc[s] = (live + a.chunk_keys - 1) / a.chunk_keys;
     total += nc[s];
   }
   const float* part = a.part + ((int64_t)(b * a.H + h) * a.n_chunks) * NQ * REC + qi * REC;
@@ -434,6 +480,36 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
   for (int i = 0; i < DPL; ++i) {
     const int dd = lane + 64 * i;
     if (dd < D) orow[dd] = A[i] * inv;
+  }
+
+  // The folded KV update of this (sequence, head), as sps_kv_update does it, from the old lengths.
+  if (upd && snap[kSnapActive] != 0) {
+    const KvUpdateArgs& u = a.upd;
+    const int64_t rlen = snap[kSnapRingLen], rpos = snap[kSnapRingPos], tlen = snap[kSnapRetLen];
+    const int64_t slot = rlen >= u.window ? rpos : rlen;
+    const bool ring_write = u.window > 0 && slot >= 0 && slot < u.ring_storage;
+    const bool ret_write = tlen >= 0 && tlen < u.ret_storage;
+    const int esz = u.kv_dtype == 2 ? 4 : 2;
+#pragma unroll
+    for (int i = 0; i < kUpdPieces; ++i) {
+      const int pc = lane + 64 * i, r = pc / upr, j = pc - r * upr;
+      if (r >= 4 || !(r < 2 ? ring_write : ret_write)) continue;
+      void* dst = r == 0 ? u.ring_k : r == 1 ? u.ring_v : r == 2 ? u.ret_k : u.ret_v;
+      const int64_t db = r == 0 ? u.rk_sb : r == 1 ? u.rv_sb : r == 2 ? u.tk_sb : u.tv_sb;
+      const int64_t dh = r == 0 ? u.rk_sh : r == 1 ? u.rv_sh : r == 2 ? u.tk_sh : u.tv_sh;
+      const int64_t dt = r == 0 ? u.rk_st : r == 1 ? u.rv_st : r == 2 ? u.tk_st : u.tv_st;
+      const int64_t t = r < 2 ? slot : tlen;
+      *reinterpret_cast<u32x4_t*>(static_cast<char*>(dst) + (b * db + h * dh + t * dt) * esz + j * 16) = uval[i];
+    }
+    if (lane == 0) {
+      if (ret_write) cache_len_store(u.ret_len, b * u.ret_len_sb + h * u.ret_len_sh, u.len_i64, tlen + 1);
+      if (h == 0 && u.window > 0) {
+        if (rlen >= u.window)
+          cache_len_store(u.ring_pos, (int64_t)b * u.ring_pos_sb, u.len_i64, (rpos + 1) % u.window);
+        else
+          cache_len_store(u.ring_len, (int64_t)b * u.ring_len_sb, u.len_i64, rlen + 1);
+      }
+    }
   }
 }
 

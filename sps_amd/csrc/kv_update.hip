@@ -18,23 +18,6 @@ namespace sps {
 
 namespace {
 
-__device__ __forceinline__ int64_t load_len(const void* p, int64_t i, int i64) {
-  return i64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t)reinterpret_cast<const int*>(p)[i];
-}
-
-__device__ __forceinline__ void store_len(void* p, int64_t i, int i64, int64_t v) {
-  if (i64)
-    reinterpret_cast<int64_t*>(p)[i] = v;
-  else
-    reinterpret_cast<int*>(p)[i] = (int)v;
-}
-
-__device__ __forceinline__ bool load_flag(const void* p, int64_t i, int bytes) {
-  if (bytes == 1) return reinterpret_cast<const uint8_t*>(p)[i] != 0;
-  if (bytes == 4) return reinterpret_cast<const int*>(p)[i] != 0;
-  return reinterpret_cast<const int64_t*>(p)[i] != 0;
-}
-
 // Copies element `src_i` of `src` (src_dtype) to element `dst_i` of `dst` (dst_dtype). Equal types
 // copy the bits; otherwise through fp32 with round-to-nearest-even (what torch's .to() does).
 __device__ __forceinline__ void copy_elem(void* dst, int64_t dst_i, int dst_dtype, const void* src, int64_t src_i,
@@ -71,12 +54,12 @@ __global__ __launch_bounds__(256) void kv_update_vec_kernel(const KvUpdateArgs a
   const int b = blockIdx.x, tid = threadIdx.x;
   // The active flag is loaded with everything else (an inactive sequence's loads are in bounds and
   // harmless) and tested once those are in flight, before anything is stored.
-  const bool act = load_flag(a.active, (int64_t)b * a.active_sb, a.active_bytes);
+  const bool act = cache_flag_load(a.active, (int64_t)b * a.active_sb, a.active_bytes);
   const bool ring = a.window > 0;
-  for (int h = tid; h < a.H; h += 256) s_len[h] = load_len(a.ret_len, b * a.ret_len_sb + h * a.ret_len_sh, a.len_i64);
+  for (int h = tid; h < a.H; h += 256) s_len[h] = cache_len_load(a.ret_len, b * a.ret_len_sb + h * a.ret_len_sh, a.len_i64);
   if (ring && tid == 0) {
-    s_ring[0] = load_len(a.ring_len, (int64_t)b * a.ring_len_sb, a.len_i64);
-    s_ring[1] = load_len(a.ring_pos, (int64_t)b * a.ring_pos_sb, a.len_i64);
+    s_ring[0] = cache_len_load(a.ring_len, (int64_t)b * a.ring_len_sb, a.len_i64);
+    s_ring[1] = cache_len_load(a.ring_pos, (int64_t)b * a.ring_pos_sb, a.len_i64);
   }
   const int esz = a.kv_dtype == 2 ? 4 : 2;
   const int ppr = a.D * esz / 16;  // 16-byte pieces per row
@@ -125,25 +108,25 @@ __global__ __launch_bounds__(256) void kv_update_vec_kernel(const KvUpdateArgs a
   }
   if (ring && tid == 0) {
     if (s_ring[0] >= a.window)
-      store_len(a.ring_pos, (int64_t)b * a.ring_pos_sb, a.len_i64, (s_ring[1] + 1) % a.window);
+      cache_len_store(a.ring_pos, (int64_t)b * a.ring_pos_sb, a.len_i64, (s_ring[1] + 1) % a.window);
     else
-      store_len(a.ring_len, (int64_t)b * a.ring_len_sb, a.len_i64, s_ring[0] + 1);
+      cache_len_store(a.ring_len, (int64_t)b * a.ring_len_sb, a.len_i64, s_ring[0] + 1);
   }
   for (int h = tid; h < a.H; h += 256) {
     const int64_t n = s_len[h];
-    if (n >= 0 && n < a.ret_storage) store_len(a.ret_len, b * a.ret_len_sb + h * a.ret_len_sh, a.len_i64, n + 1);
+    if (n >= 0 && n < a.ret_storage) cache_len_store(a.ret_len, b * a.ret_len_sb + h * a.ret_len_sh, a.len_i64, n + 1);
   }
 }
 
 // General path (dtype conversion or rows not 16-byte aligned): element by element.
 __global__ __launch_bounds__(256) void kv_update_kernel(const KvUpdateArgs a) {
   const int b = blockIdx.x, tid = threadIdx.x;
-  if (!load_flag(a.active, (int64_t)b * a.active_sb, a.active_bytes)) return;  // whole workgroup
+  if (!cache_flag_load(a.active, (int64_t)b * a.active_sb, a.active_bytes)) return;  // whole workgroup
   const bool ring = a.window > 0;
   int64_t rlen = 0, rpos = 0;
   if (ring) {
-    rlen = load_len(a.ring_len, (int64_t)b * a.ring_len_sb, a.len_i64);
-    rpos = load_len(a.ring_pos, (int64_t)b * a.ring_pos_sb, a.len_i64);
+    rlen = cache_len_load(a.ring_len, (int64_t)b * a.ring_len_sb, a.len_i64);
+    rpos = cache_len_load(a.ring_pos, (int64_t)b * a.ring_pos_sb, a.len_i64);
   }
   const bool full = rlen >= a.window;
   const int64_t slot = full ? rpos : rlen;
@@ -157,7 +140,7 @@ __global__ __launch_bounds__(256) void kv_update_kernel(const KvUpdateArgs a) {
       copy_elem(a.ring_v, b * a.rv_sb + h * a.rv_sh + slot * a.rv_st + d, a.kv_dtype, a.vw,
                 b * a.vw_sb + h * a.vw_sh + d, a.new_dtype);
     }
-    const int64_t len = load_len(a.ret_len, b * a.ret_len_sb + h * a.ret_len_sh, a.len_i64);
+    const int64_t len = cache_len_load(a.ret_len, b * a.ret_len_sb + h * a.ret_len_sh, a.len_i64);
     if (len >= 0 && len < a.ret_storage) {
       copy_elem(a.ret_k, b * a.tk_sb + h * a.tk_sh + len * a.tk_st + d, a.kv_dtype, a.kr,
                 b * a.kr_sb + h * a.kr_sh + d, a.new_dtype);
@@ -168,14 +151,14 @@ __global__ __launch_bounds__(256) void kv_update_kernel(const KvUpdateArgs a) {
   __syncthreads();  // every thread has read the old lengths before any is advanced
   if (ring && tid == 0) {
     if (full)
-      store_len(a.ring_pos, (int64_t)b * a.ring_pos_sb, a.len_i64, (rpos + 1) % a.window);
+      cache_len_store(a.ring_pos, (int64_t)b * a.ring_pos_sb, a.len_i64, (rpos + 1) % a.window);
     else
-      store_len(a.ring_len, (int64_t)b * a.ring_len_sb, a.len_i64, rlen + 1);
+      cache_len_store(a.ring_len, (int64_t)b * a.ring_len_sb, a.len_i64, rlen + 1);
   }
   for (int h = tid; h < a.H; h += 256) {
     const int64_t off = b * a.ret_len_sb + h * a.ret_len_sh;
-    const int64_t len = load_len(a.ret_len, off, a.len_i64);
-    if (len >= 0 && len < a.ret_storage) store_len(a.ret_len, off, a.len_i64, len + 1);
+    const int64_t len = cache_len_load(a.ret_len, off, a.len_i64);
+    if (len >= 0 && len < a.ret_storage) cache_len_store(a.ret_len, off, a.len_i64, len + 1);
   }
 }
 

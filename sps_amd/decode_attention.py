@@ -69,10 +69,13 @@ def _as_attn(t: Tensor, attn_dtype: torch.dtype) -> Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
-def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor, static_scratch: bool = False) -> Tensor:
+def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor, static_scratch: bool = False,
+                kv_update: Optional[tuple] = None) -> Tensor:
     """Calls sps_decode. q: [B, nq, H, D] (bf16/f16/f32); extras: list of (k, v) [B, H, D] sharing one
     dtype and one (b, h) stride pair. ``static_scratch`` calls sps_decode_static instead, which keeps
-    its partial records in the library's own scratch array (no workspace is allocated)."""
+    its partial records in the library's own scratch array (no workspace is allocated). ``kv_update``
+    (the argument tuple of decode_attention_fast.kv_update_args) calls sps_decode_kv_update instead:
+    the same attention, then that KV update of the caches, in the attention's launches."""
     b, _, h, d = q.shape
     kv_dtype = N.DTYPE_BF16
     if segments:
@@ -82,7 +85,13 @@ def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor, 
     lib = N.lib()
     scan_arr = N.i64_array(scans)
     ws = None
-    if not static_scratch:
+    if kv_update is not None:
+        upd = kv_update[0]
+        if segments and upd[3] != kv_dtype:
+            raise RuntimeError("decode with KV update: the caches must have the segments' dtype")
+        ws_bytes = lib.sps_decode_kv_update_workspace_bytes(b, h, d, nq, kv_dtype, len(segments), scan_arr)
+        ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
+    elif not static_scratch:
         ws_bytes = lib.sps_decode_workspace_bytes(b, h, d, nq, kv_dtype, len(segments), scan_arr)
         ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
     k_strides, v_strides = [], []
@@ -93,8 +102,13 @@ def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor, 
     ev = [e[1] for e in extras]
     e_strides = (ek[0].stride(0), ek[0].stride(1)) if extras else (0, 0)
     e_dtype = _KV_DTYPES[ek[0].dtype] if extras else N.DTYPE_F32
-    tail = () if static_scratch else (ws.data_ptr(), ws.numel())
-    entry = lib.sps_decode_static if static_scratch else lib.sps_decode
+    if kv_update is not None:
+        name, entry, tail = "sps_decode_kv_update", lib.sps_decode_kv_update, (*kv_update[0][4:-1], ws.data_ptr(),
+                                                                                ws.numel())
+    elif static_scratch:
+        name, entry, tail = "sps_decode_static", lib.sps_decode_static, ()
+    else:
+        name, entry, tail = "sps_decode", lib.sps_decode, (ws.data_ptr(), ws.numel())
     status = entry(
         b, h, d, nq,
         q.data_ptr(), _KV_DTYPES[q.dtype], N.i64_array((q.stride(0), q.stride(1), q.stride(2))),
@@ -108,7 +122,7 @@ def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor, 
         1.0 / math.sqrt(d), out.data_ptr(), N.i64_array((out.stride(0), out.stride(1), out.stride(2))),
         *tail, torch.cuda.current_stream(q.device).cuda_stream,
     )
-    N.check("sps_decode_static" if static_scratch else "sps_decode", status)
+    N.check(name, status)
     return out
 
 
@@ -153,11 +167,13 @@ def triton_segmented_q1_attention(
     *,
     extra_kv: list[tuple[Tensor, Tensor]] | None = None,
     attn_dtype: torch.dtype,
+    _kv_update: Optional[tuple] = None,
 ) -> Optional[Tensor]:
     """One query per (batch, head) over <= 3 segments plus <= 2 always-visible extra keys.
 
     Returns fp32 [B, H, D], or None when the inputs are outside what the kernel supports (the
-    reference's contract: the caller then falls back).
+    reference's contract: the caller then falls back). ``_kv_update`` is internal
+    (decode_attention_fast.segmented_q1_attention_with_kv_update).
     """
     if not q_BxHxD.is_cuda:
         return None
@@ -180,7 +196,7 @@ def triton_segmented_q1_attention(
     q4 = _as_attn(q_BxHxD, attn_dtype).unsqueeze(1)
     out = torch.empty((batch_size, n_head, head_dim), device=q_BxHxD.device, dtype=torch.float32)
     out4 = out.view(batch_size, 1, n_head, head_dim)
-    _run_decode(q4, 1, list(segments), extras, [1] * len(extras), out4)
+    _run_decode(q4, 1, list(segments), extras, [1] * len(extras), out4, kv_update=_kv_update)
     return out
 
 
@@ -193,10 +209,12 @@ def triton_segmented_q2_attention(
     current_predict_k_BxHxD: Tensor,
     current_predict_v_BxHxD: Tensor,
     attn_dtype: torch.dtype,
+    _kv_update: Optional[tuple] = None,
 ) -> Tensor:
     """Two queries per (batch, head): slot 0 (input) sees the segments + current input key; slot 1
     (<predict>) additionally sees the current <predict> key. Fail-fast: raises RuntimeError on any
-    unsupported input, as the reference does. Returns fp32 [B, 2, H, D]."""
+    unsupported input, as the reference does. Returns fp32 [B, 2, H, D]. ``_kv_update`` is internal
+    (decode_attention_fast.segmented_q2_attention_with_kv_update)."""
     if not q_Bx2xHxD.is_cuda:
         raise RuntimeError("CUDA tensors are required for SPS-family cached generation attention")
     if len(segments) > 2:
@@ -243,7 +261,7 @@ def triton_segmented_q2_attention(
                          (current_predict_k_BxHxD, current_predict_v_BxHxD)], attn_dtype, batch_size, n_head, head_dim)
     q = _as_attn(q_Bx2xHxD, attn_dtype)
     out = torch.empty((batch_size, 2, n_head, head_dim), device=q_Bx2xHxD.device, dtype=torch.float32)
-    return _run_decode(q, 2, list(segments), extras, [0b11, 0b10], out)
+    return _run_decode(q, 2, list(segments), extras, [0b11, 0b10], out, kv_update=_kv_update)
 
 
 def masked_kv_attention(

@@ -167,3 +167,25 @@ def test_rope_argument_validation():
     assert _rope(in_dtype=N.DTYPE_I32) == N.SPS_E_UNSUPPORTED and "input dtype" in N.last_error()
     assert _rope(ptr=0x10004) == N.SPS_E_INVALID and "aligned" in N.last_error()
     assert _rope(st=(4096, 66, 64)) == N.SPS_E_INVALID and "aligned" in N.last_error()
+
+
+def _decode_kv_update(len_dtype=N.DTYPE_I64, nq=1, window=2, ring_storage=4, ws_bytes=1 << 20):
+    z = N.i64_array([0] * 8)
+    p = 0x1000
+    return N.lib().sps_decode_kv_update(
+        1, 1, 64, nq, 0x1000, N.DTYPE_BF16, z, N.DTYPE_BF16, 0, None, z, None, z, None, None, None, z, 0, None, None,
+        N.DTYPE_BF16, z, None, 0.125, 0x2000, z,
+        p, p, z, ring_storage, window, p, p, z, p, p, z, 8, p, z, len_dtype, N.DTYPE_BF16, p, p, p, p, z, p,
+        N.DTYPE_U8, 1, 0x50000, ws_bytes, None)
+
+
+@cpu_only
+def test_decode_kv_update_argument_validation():
+    # The update's arguments are checked before the decode's, and nothing is launched on failure.
+    assert _decode_kv_update(len_dtype=N.DTYPE_F32) == N.SPS_E_INVALID and "lengths" in N.last_error()
+    assert _decode_kv_update(window=5) == N.SPS_E_INVALID and "ring storage" in N.last_error()
+    assert _decode_kv_update(nq=3) == N.SPS_E_INVALID and "nq" in N.last_error()
+    scans = N.i64_array([64, 4096])
+    lib = N.lib()
+    assert lib.sps_decode_kv_update_workspace_bytes(64, 16, 64, 1, N.DTYPE_BF16, 2, scans) >= \
+        lib.sps_decode_workspace_bytes(64, 16, 64, 1, N.DTYPE_BF16, 2, scans) + 64 * 16 * 8 * 8
