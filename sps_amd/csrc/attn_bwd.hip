@@ -292,7 +292,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(dq_waves<D>
   bool staged = false;
   if constexpr (D >= 64) {
     if (rows16_ok(a.dq, a.sdq)) {
-      store_rows_via_lds<D>(wave_tile(sK, wave), lane, orow, qvalid, piece);
+      const int q0 = tp.tile * kTile + wave * kBlock;
+      store_rows_via_lds<D>(wave_tile(sK, wave), lane, a.dq + b * a.sdq.b + h * a.sdq.h + (int64_t)q0 * a.sdq.n,
+                            a.sdq.n, imin(kBlock, m.N - q0), piece);
       staged = true;
     }
   }
@@ -616,10 +618,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(bwd_waves<D
   bool staged = false;
   if constexpr (kDma) {
     if (rows16_ok(a.dk, a.sdk) && rows16_ok(a.dv, a.sdv)) {
-      uint16_t* krow = a.dk + b * a.sdk.b + h * a.sdk.h + (int64_t)kp * a.sdk.n;
-      uint16_t* vrow = a.dv + b * a.sdv.b + h * a.sdv.h + (int64_t)kp * a.sdv.n;
-      store_rows_via_lds<D>(wave_tile(sQ, wave), lane, krow, kvalid, piece_k);
-      store_rows_via_lds<D>(wave_tile(sDO, wave), lane, vrow, kvalid, piece_v);
+      // The wave's keys are consecutive indices of one stream: rows `step` positions apart.
+      const int t0 = st.first + wave * kBlock;
+      const int p0 = stream_pos(m, st.stream, t0);
+      const int nrows = imin(kBlock, stream_len(m.family, m.N, st.stream, m.P) - t0);
+      const int kstep = m.family == FAMILY_FULL ? 1 : 2;
+      store_rows_via_lds<D>(wave_tile(sQ, wave), lane, a.dk + b * a.sdk.b + h * a.sdk.h + (int64_t)p0 * a.sdk.n,
+                            kstep * a.sdk.n, nrows, piece_k);
+      store_rows_via_lds<D>(wave_tile(sDO, wave), lane, a.dv + b * a.sdv.b + h * a.sdv.h + (int64_t)p0 * a.sdv.n,
+                            kstep * a.sdv.n, nrows, piece_v);
       staged = true;
     }
   }

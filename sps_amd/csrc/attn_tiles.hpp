@@ -575,11 +575,12 @@ __device__ __forceinline__ void run_pairs(int nb, Issue&& issue, Put&& put, Body
 // row c32, elements d = 32 dc + 8 ii + 4 g .. +3 as 8-byte pieces from piece(dc, ii)) through the
 // wave's own idle LDS tile (at least 32 * D elements), so that each global store writes 16 bytes and
 // CPR lanes cover a whole row (half the store instructions of the direct 8-byte stores, each
-// covering whole rows instead of a 16-byte piece of 32 rows). `row` is the lane's own row pointer,
-// `valid` whether that row exists; the wave reads back only what it wrote (LDS operations of one
-// wave complete in order), so no barrier is needed.
+// covering whole rows instead of a 16-byte piece of 32 rows). Row r of the wave starts at
+// row0 + r * row_stride (elements; wave-uniform) and exists for r < nrows; the wave reads back only
+// what it wrote (LDS operations of one wave complete in order), so no barrier is needed.
 template <int D, class PieceFn>
-__device__ __forceinline__ void store_rows_via_lds(uint16_t* tile, int lane, uint16_t* row, bool valid, PieceFn piece) {
+__device__ __forceinline__ void store_rows_via_lds(uint16_t* tile, int lane, uint16_t* row0, int64_t row_stride,
+                                                   int nrows, PieceFn piece) {
   static_assert(D >= 64 && D % 64 == 0, "the chunk swizzle needs at least 8 chunks per row");
   constexpr int CPR = D / 8;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;  // rows per store instruction
@@ -594,15 +595,11 @@ __device__ __forceinline__ void store_rows_via_lds(uint16_t* tile, int lane, uin
       *reinterpret_cast<SPS_LDS u32x2_t*>((SPS_LDS uint16_t*)(tile + off)) = piece(dc, ii);
     }
   }
-  const uint64_t rp = reinterpret_cast<uint64_t>(row);
 #pragma unroll
   for (int k = 0; k < kBlock / RPI; ++k) {
     const int r = k * RPI + lane / CPR, ch = lane % CPR;
-    const uint64_t rp_r = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(rp >> 32), r) << 32) |
-                          (uint32_t)__shfl((int)(uint32_t)rp, r);
-    const bool v_r = __shfl((int)valid, r) != 0;
     const u32x4_t x = lds_read_b128(tile + r * D + (ch ^ (r & 7)) * 8);
-    if (v_r) *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(rp_r) + ch * 8) = x;
+    if (r < nrows) *reinterpret_cast<u32x4_t*>(row0 + r * row_stride + ch * 8) = x;
   }
 }
 
