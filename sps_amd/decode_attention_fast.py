@@ -140,44 +140,77 @@ def fused_sps_kv_update(
         v_retained_BxHxD=v_retained_BxHxD, active_mask_B=active_mask_B, window_tokens=window_tokens))
 
 
-def _update_kwargs(kw: dict) -> dict:
-    names = ("nw_k", "nw_v", "nw_len", "nw_pos", "br_k", "br_v", "br_len", "k_window_BxHxD", "v_window_BxHxD",
-             "k_retained_BxHxD", "v_retained_BxHxD", "active_mask_B", "window_tokens")
-    missing = [n for n in names if n not in kw]
-    extra = [n for n in kw if n not in names]
-    if missing or extra:
-        raise TypeError(f"KV update arguments: missing {missing}, unexpected {extra}")
-    return kw
-
-
-def segmented_q2_attention_with_kv_update(q_Bx2xHxD: Tensor, segments, *, current_normal_k_BxHxD: Tensor,
-                                          current_normal_v_BxHxD: Tensor, current_predict_k_BxHxD: Tensor,
-                                          current_predict_v_BxHxD: Tensor, attn_dtype: torch.dtype,
-                                          **kv_update) -> Tensor:
+def segmented_q2_attention_with_kv_update(
+    q_Bx2xHxD: Tensor,
+    segments,
+    *,
+    current_normal_k_BxHxD: Tensor,
+    current_normal_v_BxHxD: Tensor,
+    current_predict_k_BxHxD: Tensor,
+    current_predict_v_BxHxD: Tensor,
+    attn_dtype: torch.dtype,
+    nw_k: Tensor,
+    nw_v: Tensor,
+    nw_len: Tensor,
+    nw_pos: Tensor,
+    br_k: Tensor,
+    br_v: Tensor,
+    br_len: Tensor,
+    k_window_BxHxD: Tensor,
+    v_window_BxHxD: Tensor,
+    k_retained_BxHxD: Tensor,
+    v_retained_BxHxD: Tensor,
+    active_mask_B: Tensor,
+    window_tokens: int,
+) -> Tensor:
     """One decode step of one layer in the attention's launches: ``triton_segmented_q2_attention``
     over the caches (as they are before the update), then ``fused_sps_kv_update`` of the same caches
-    with the keyword arguments of that function (``nw_k`` ... ``window_tokens``). This is the pair the
-    reference's generation step runs back to back (reverse_sps/inference.py:322-362, then the update
-    of :169-238 via ``_update_normal_memory`` / ``_update_predict_memory``). Returns fp32 [B, 2, H, D];
-    the caches and lengths are updated in place. The caches must have the segments' dtype."""
+    (the keyword arguments from ``nw_k`` on are that function's). This is the pair the reference's
+    generation step runs back to back (reverse_sps/inference.py:322-362, then the update of :169-238
+    via ``_update_normal_memory`` / ``_update_predict_memory``). Returns fp32 [B, 2, H, D]; the caches
+    and lengths are updated in place. The caches must have the segments' dtype."""
     from .decode_attention import triton_segmented_q2_attention
 
-    upd = kv_update_args(**_update_kwargs(kv_update))
+    upd = kv_update_args(
+        nw_k=nw_k, nw_v=nw_v, nw_len=nw_len, nw_pos=nw_pos, br_k=br_k, br_v=br_v, br_len=br_len,
+        k_window_BxHxD=k_window_BxHxD, v_window_BxHxD=v_window_BxHxD, k_retained_BxHxD=k_retained_BxHxD,
+        v_retained_BxHxD=v_retained_BxHxD, active_mask_B=active_mask_B, window_tokens=window_tokens)
     return triton_segmented_q2_attention(
         q_Bx2xHxD, segments, current_normal_k_BxHxD=current_normal_k_BxHxD,
         current_normal_v_BxHxD=current_normal_v_BxHxD, current_predict_k_BxHxD=current_predict_k_BxHxD,
         current_predict_v_BxHxD=current_predict_v_BxHxD, attn_dtype=attn_dtype, _kv_update=upd)
 
 
-def segmented_q1_attention_with_kv_update(q_BxHxD: Tensor, segments, *, extra_kv=None, attn_dtype: torch.dtype,
-                                          **kv_update) -> Tensor:
+def segmented_q1_attention_with_kv_update(
+    q_BxHxD: Tensor,
+    segments,
+    *,
+    extra_kv=None,
+    attn_dtype: torch.dtype,
+    nw_k: Tensor,
+    nw_v: Tensor,
+    nw_len: Tensor,
+    nw_pos: Tensor,
+    br_k: Tensor,
+    br_v: Tensor,
+    br_len: Tensor,
+    k_window_BxHxD: Tensor,
+    v_window_BxHxD: Tensor,
+    k_retained_BxHxD: Tensor,
+    v_retained_BxHxD: Tensor,
+    active_mask_B: Tensor,
+    window_tokens: int,
+) -> Tensor:
     """As segmented_q2_attention_with_kv_update for one query per (batch, head): the attention of
-    ``triton_segmented_q1_attention`` (the reference's decode of the <predict> slot through
+    ``triton_segmented_q1_attention`` (the reference's decode of one slot through
     ``masked_kv_attention``, reverse_sps/inference.py:270-320), then ``fused_sps_kv_update``. Returns
     fp32 [B, H, D]; raises RuntimeError where the q1 kernel does not apply (there is no other path)."""
     from .decode_attention import triton_segmented_q1_attention
 
-    upd = kv_update_args(**_update_kwargs(kv_update))
+    upd = kv_update_args(
+        nw_k=nw_k, nw_v=nw_v, nw_len=nw_len, nw_pos=nw_pos, br_k=br_k, br_v=br_v, br_len=br_len,
+        k_window_BxHxD=k_window_BxHxD, v_window_BxHxD=v_window_BxHxD, k_retained_BxHxD=k_retained_BxHxD,
+        v_retained_BxHxD=v_retained_BxHxD, active_mask_B=active_mask_B, window_tokens=window_tokens)
     out = triton_segmented_q1_attention(q_BxHxD, segments, extra_kv=extra_kv, attn_dtype=attn_dtype, _kv_update=upd)
     if out is None:
         raise RuntimeError("segmented_q1_attention_with_kv_update: inputs outside what the decode kernel supports")

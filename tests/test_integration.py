@@ -143,3 +143,19 @@ def test_without_the_modeling_package_gpu_calls_only(monkeypatch):
     assert "modeling.models.attention.triton_full_flash_attention" in touched
     with pytest.raises(RuntimeError, match="GPU only"):
         sps_amd.masked_kv_attention(torch.zeros(1, 1, 64), [], attn_dtype=torch.float32)
+
+
+def test_fused_decode_wrappers_take_both_reference_signatures():
+    # segmented_q{1,2}_attention_with_kv_update take the keyword arguments of the attention call they
+    # replace (triton_segmented_q{1,2}_attention) followed by fused_sps_kv_update's, under the same names.
+    import inspect
+
+    from sps_amd import decode_attention as DA
+    from sps_amd import decode_attention_fast as DF
+
+    upd = [p for p in inspect.signature(DF.fused_sps_kv_update).parameters]
+    for fused, attn in ((DF.segmented_q2_attention_with_kv_update, DA.triton_segmented_q2_attention),
+                        (DF.segmented_q1_attention_with_kv_update, DA.triton_segmented_q1_attention)):
+        got = list(inspect.signature(fused).parameters)
+        want = [p for p in inspect.signature(attn).parameters if not p.startswith("_")] + upd
+        assert got == want, (fused.__name__, got, want)
