@@ -59,6 +59,7 @@ struct AttnArgs {
   TilePlan* q_plan;  // [B, q_tiles] query-tile plans, heaviest first
   TilePlan* k_plan;  // [B, k_tiles] key-tile plans, heaviest first
   int B, H;
+  FastDiv div_bh, div_b, div_h;  // B H, B and H (workgroup -> row, head, rank)
   float sm_scale;
   float scale2;  // sm_scale * log2(e)
   MaskSpec m;

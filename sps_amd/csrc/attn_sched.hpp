@@ -59,6 +59,27 @@ struct Interval {
 __host__ __device__ __forceinline__ int imin(int x, int y) { return x < y ? x : y; }
 __host__ __device__ __forceinline__ int imax(int x, int y) { return x > y ? x : y; }
 
+// Division by a divisor fixed at launch (the grid's batch rows, heads, row x head slots), for
+// dividends below 2^31: q = (mulhi(x, mul) + x) >> shift with shift = ceil(log2 d) and
+// mul = floor(2^32 (2^shift - d) / d) + 1 (Granlund & Montgomery, "Division by invariant integers
+// using multiplication", 1994: the round-up method; the sum stays below 2^32 since mulhi(x, mul) <= x).
+// The kernels divide wave-uniform values, so this is a few scalar instructions, where a division
+// by a runtime divisor is a VALU sequence of ~20 instructions.
+struct FastDiv {
+  uint32_t d, mul, shift;
+};
+
+inline FastDiv make_fast_div(uint32_t d) {
+  if (d == 0) return FastDiv{0, 0, 0};  // no grid to map
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  return FastDiv{d, (uint32_t)((((1ull << 32) * ((1ull << l) - d)) / d) + 1), l};
+}
+
+__host__ __device__ __forceinline__ uint32_t fast_div(uint32_t x, const FastDiv& f) {
+  return ((uint32_t)(((uint64_t)x * f.mul) >> 32) + x) >> f.shift;
+}
+
 __host__ __device__ __forceinline__ int stream_parity(const MaskSpec& m, int stream) {
   return stream == STREAM_PERSISTENT ? m.P : 1 - m.P;
 }

@@ -317,8 +317,16 @@ __device__ __forceinline__ bool q_begin(const AttnArgs& a, const TilePlan& tp, c
 // rows would drain and idle while the others still hold work only they may start (measured: ~8% of
 // the attention time at the benchmark shape). When H is a multiple of the XCD count the rotation
 // keeps every (row, head) on one XCD, so its K/V tiles stay in that XCD's L2.
-__device__ __forceinline__ int row_rotation(int j, int rank, int H, int BH) {
-  return (int)(((int64_t)j + (int64_t)rank * H) % BH);
+// Slot j (< B H) of rank `rank` -> (row, head) index (j + rank H) mod B H, as j + (rank mod B) H
+// less B H when that reaches B H (rank H mod B H = (rank mod B) H).
+__device__ __forceinline__ void workgroup_slot(const AttnArgs& a, int& b, int& h, int& rank) {
+  const int BH = a.B * a.H;
+  rank = (int)fast_div(blockIdx.x, a.div_bh);
+  const int j = (int)blockIdx.x - rank * BH;
+  int bh = j + (rank - (int)fast_div((uint32_t)rank, a.div_b) * a.B) * a.H;
+  if (bh >= BH) bh -= BH;
+  b = (int)fast_div((uint32_t)bh, a.div_h);
+  h = bh - b * a.H;
 }
 
 __device__ __forceinline__ TilePlan uniform_plan(const TilePlan& p) {
@@ -327,10 +335,8 @@ __device__ __forceinline__ TilePlan uniform_plan(const TilePlan& p) {
 }
 
 __device__ __forceinline__ void q_workgroup(const AttnArgs& a, int& b, int& h, TilePlan& tp) {
-  const int BH = a.B * a.H;
-  const int rank = blockIdx.x / BH, bh = row_rotation(blockIdx.x - rank * BH, rank, a.H, BH);
-  b = bh / a.H;
-  h = bh - b * a.H;
+  int rank;
+  workgroup_slot(a, b, h, rank);
   tp = uniform_plan(q_plan_of(a, b, rank));
 }
 
@@ -412,10 +418,8 @@ __device__ __forceinline__ bool k_begin(const AttnArgs& a, const TilePlan& tp, c
 }
 
 __device__ __forceinline__ void k_workgroup(const AttnArgs& a, int& b, int& h, TilePlan& tp) {
-  const int BH = a.B * a.H;
-  const int rank = blockIdx.x / BH, bh = row_rotation(blockIdx.x - rank * BH, rank, a.H, BH);
-  b = bh / a.H;
-  h = bh - b * a.H;
+  int rank;
+  workgroup_slot(a, b, h, rank);
   tp = uniform_plan(k_plan_of(a, b, rank));
 }
 

@@ -118,6 +118,9 @@ int setup_common(sps::AttnArgs& a, int family, int B, int H, int N, const void* 
   a.seeds = backward ? reinterpret_cast<float*>(ws + l.seeds) : nullptr;
   a.B = B;
   a.H = H;
+  a.div_bh = sps::make_fast_div((uint32_t)(B * H));
+  a.div_b = sps::make_fast_div((uint32_t)B);
+  a.div_h = sps::make_fast_div((uint32_t)H);
   a.m.family = family;
   a.m.P = family == SPS_FAMILY_REVERSE_SPS ? 1 : 0;
   a.m.N = N;

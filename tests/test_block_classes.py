@@ -49,3 +49,19 @@ def test_closed_form_tile_plans(tmp_path):
     out = subprocess.run([str(exe), "20000"], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stdout + out.stderr
     assert out.stdout.strip().endswith("bad 0")
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(),
+                    reason="hipcc not available")
+def test_fast_division_and_slot_rotation(tmp_path):
+    # The attention kernels map workgroups to (row, head, rank) with fast_div (multiply-high by a
+    # launch-time reciprocal); the host check compares it with integer division, exhaustively for
+    # small divisors and dividends and at random up to 2^31, and the slot rotation with its
+    # definition (j + rank H) mod B H.
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    exe = tmp_path / "fast_div_check"
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-O2", "-std=c++17", "-w",
+                    str(HERE / "native" / "fast_div_check.hip"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe), "20000"], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert out.stdout.strip().endswith("bad 0")
