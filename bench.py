@@ -673,7 +673,7 @@ def cpu_decode_baseline(cfg, budget_s: float):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU work per baseline leg")
