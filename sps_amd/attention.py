@@ -15,7 +15,6 @@ no padding of N to a multiple of 128 (the kernels bounds-check), no ``.contiguou
 
 from __future__ import annotations
 
-import math
 from typing import Optional, Tuple
 
 import torch
@@ -317,7 +316,3 @@ def attention_mask(family: int, n: int, documents_idx_BxT: Optional[torch.Tensor
     )
     N.check("sps_attn_mask", status)
     return mask
-
-
-def default_sm_scale(head_dim: int) -> float:
-    return 1.0 / math.sqrt(head_dim)

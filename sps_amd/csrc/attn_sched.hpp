@@ -238,18 +238,6 @@ __host__ __device__ __forceinline__ int classify_block(const WaveSpan& w, int t0
 // Row of a 32x32 MFMA accumulator held in element i by a lane of half g (= lane / 32).
 __device__ __forceinline__ int acc_row(int i, int g) { return 8 * (i >> 2) + 4 * g + (i & 3); }
 
-// Bit i set when row acc_row(i, g) of a block starting at t0 lies in [lo, hi].
-__device__ __forceinline__ uint32_t interval_bits(int lo, int hi, int t0, int g) {
-  const int a = lo - t0 - 4 * g, z = hi - t0 - 4 * g;
-  uint32_t bits = 0;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int r = 8 * (i >> 2) + (i & 3);
-    bits |= (uint32_t)(r >= a && r <= z) << i;
-  }
-  return bits;
-}
-
 // ---------------------------------------------------------------------------------------------
 // Workgroup tiles and their order. Query-stationary kernels (forward, dQ) own kTile consecutive
 // positions; the key-stationary kernel (dK/dV) owns kTile consecutive indices of one stream

@@ -613,24 +613,10 @@ __device__ __forceinline__ bool rows16_ok(const void* p, const Strides3& st) {
   return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && ((st.b | st.h | st.n) & 7) == 0;
 }
 
-// Maximum of the 32 elements of two accumulators as a shallow tree of gfx950's 3-input IEEE
-// maximum (v_maximum3_f32: NaN-propagating, so unlike fmaxf it needs no quieting of the MFMA
-// results first; the loops are latency-bound, so the reduction depth matters more than its
-// instruction count).
+// gfx950's 3-input IEEE maximum (v_maximum3_f32: NaN-propagating, so unlike fmaxf it needs no
+// quieting of the MFMA results first).
 __device__ __forceinline__ float max3f(float a, float b, float c) {
   return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
-}
-
-__device__ __forceinline__ float max32(const f32x16_t& s, const f32x16_t& t) {
-  float m[11];
-#pragma unroll
-  for (int k = 0; k < 5; ++k) m[k] = max3f(s[3 * k], s[3 * k + 1], s[3 * k + 2]);
-#pragma unroll
-  for (int k = 0; k < 5; ++k) m[5 + k] = max3f(t[3 * k], t[3 * k + 1], t[3 * k + 2]);
-  m[10] = __builtin_elementwise_maximum(s[15], t[15]);
-  const float x = max3f(m[0], m[1], m[2]), y = max3f(m[3], m[4], m[5]);
-  const float z = max3f(m[6], m[7], m[8]);
-  return max3f(x, y, max3f(z, m[9], m[10]));
 }
 
 }  // namespace sps

@@ -169,15 +169,6 @@ __device__ __forceinline__ void lds_dma_b32(BufRsrc r, float* lds, uint32_t voff
 // for registers loaded before the loop.
 __device__ __forceinline__ void vmem_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// s_waitcnt vmcnt(N) (expcnt and lgkmcnt not waited on): at most N vector-memory loads of the wave
-// remain outstanding. Loads complete in issue order for this counter, so it waits for every load but
-// the last N issued.
-template <int N>
-__device__ __forceinline__ void vmem_wait_le() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 // Reads a value that is uniform across the wave into a scalar register.
 __device__ __forceinline__ int wave_uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
