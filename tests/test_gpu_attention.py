@@ -127,6 +127,34 @@ def test_parity_matrix(case):
     _check(family, b, h, n, d, window=w, docs=docs, pkw=pkw, dtype=dtype, layout=layout, seed=n)
 
 
+TINY_CASES = [
+    # family, n, d, window, docs: the smallest sequences each family accepts (one partial block)
+    ("full", 1, 64, 0, None),
+    ("full", 3, 16, 0, [[0, 1, 1]]),
+    ("sps", 2, 64, 0, None),
+    ("sps", 4, 32, 1, [[0, 0, 1, 1]]),
+    ("sps", 6, 128, 64, [[0, 0, 0, 0, 0, 0]]),
+    ("reverse_sps", 2, 64, -1, None),
+    ("reverse_sps", 4, 64, 3, [[5, 5, 7, 7]]),
+]
+
+
+@pytest.mark.parametrize("case", TINY_CASES, ids=[f"{c[0]}-n{c[1]}-d{c[2]}-w{c[3]}" for c in TINY_CASES])
+def test_tiny_sequences(case):
+    family, n, d, w, docs = case
+    _check(family, 1, 2, n, d, window=w, docs=None if docs is None else np.array(docs, dtype=np.int64),
+           seed=n + d)
+
+
+def test_empty_batch():
+    # No (batch, head) slice: empty outputs and gradients, no launch.
+    q, k, v = (torch.randn(0, 2, 64, 64, device="cuda", dtype=torch.bfloat16).requires_grad_() for _ in range(3))
+    out = SA.sps_sliding_attention(q, k, v, 0.125, 64)
+    assert out.shape == (0, 2, 64, 64)
+    out.sum().backward()
+    assert q.grad.shape == q.shape and k.grad.shape == k.shape and v.grad.shape == v.shape
+
+
 def test_int32_documents():
     rng = np.random.default_rng(1)
     docs = _packed_docs(rng, 2, 160, "sps")
