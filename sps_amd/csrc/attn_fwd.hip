@@ -109,12 +109,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, 8))) voi
   u32x4_t qf[D / 16];
   {
     const uint16_t* qrow = a.q + b * a.sq.b + h * a.sq.h + (int64_t)(qvalid ? qp : 0) * a.sq.n;
-    const uint32_t sign = flip_q ? 0x80008000u : 0u;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
       u32x4_t z = {0u, 0u, 0u, 0u};
       qf[c] = qvalid ? *reinterpret_cast<const u32x4_t*>(qrow + 16 * c + 8 * g) : z;
-      qf[c] ^= sign;
+    }
+    if (flip_q) {
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) qf[c] ^= 0x80008000u;
     }
   }
 
@@ -242,11 +244,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W, 8))) voi
           const float mb = raw * scale2;
           const float m_new = need ? mb : m_run;
           const float alpha = need ? fast_exp2(m_run - m_new) : 1.f;
+          // While no lane has seen a score the sums and accumulators are still zero: nothing to scale.
+          if (wave_any(m_run != -INFINITY)) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) l_run[r] *= alpha;
+#pragma unroll
+            for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
+          }
           m_run = m_new;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) l_run[r] *= alpha;
-#pragma unroll
-          for (int dc = 0; dc < G::DC; ++dc) acc[dc] *= alpha;
           negm = m_run == -INFINITY ? 0.f : -m_run;
           thr = m_run == -INFINITY ? -INFINITY : (m_run + kRescaleThreshold) * inv_scale2;
         }
