@@ -199,6 +199,21 @@ def i64_array(values) -> C.Array:
     return (C.c_int64 * max(len(vals), 1))(*vals)
 
 
+_I64_CACHE: dict = {}
+
+
+def i64_const(values: tuple) -> C.Array:
+    """i64_array of a tuple of ints, cached by value, for stride and size arguments of per-call host
+    paths: the native entry points only read these arrays during the call and nothing writes them,
+    so equal tuples can share one array (the cache is emptied past 1024 entries)."""
+    arr = _I64_CACHE.get(values)
+    if arr is None:
+        if len(_I64_CACHE) >= 1024:
+            _I64_CACHE.clear()
+        arr = _I64_CACHE[values] = i64_array(values)
+    return arr
+
+
 def i32_array(values) -> C.Array:
     vals = list(values)
     return (C.c_int * max(len(vals), 1))(*vals)

@@ -19,9 +19,11 @@ _FLOAT_DTYPES = {torch.bfloat16: N.DTYPE_BF16, torch.float16: N.DTYPE_F16, torch
 _LEN_DTYPES = {torch.int32: N.DTYPE_I32, torch.int64: N.DTYPE_I64}
 
 
-def _aligned(t: Tensor) -> bool:
-    el = t.element_size()
-    return t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * el) % 16 == 0 for s in t.stride()[:-1])
+def _rows16(ptr: int, strides: tuple, el: int) -> bool:
+    """For a 4-D tensor: unit last stride, and every row start 16-byte aligned (base and the three
+    outer strides; with a power-of-two element size, one test of the strides' OR covers all three)."""
+    s0, s1, s2, s3 = strides
+    return s3 == 1 and ptr % 16 == 0 and ((s0 | s1 | s2) * el) % 16 == 0
 
 
 def prefill_to_decode(k_Bx2TxHxD: Tensor, v_Bx2TxHxD: Tensor, current_doc_mask_BxT: Tensor, *, window_slot: int,
@@ -29,54 +31,72 @@ def prefill_to_decode(k_Bx2TxHxD: Tensor, v_Bx2TxHxD: Tensor, current_doc_mask_B
                       br_k: Tensor, br_v: Tensor, br_len: Tensor, window_tokens: int) -> None:
     """Writes one layer's decode caches from the prefill K/V (in place). Shapes: K/V [B, 2T, H, D];
     mask [B, T] bool; ring caches [B, H, Sw, D] with lengths/positions [B]; retained caches
-    [B, H, Sr, D] with lengths [B, H]. The ring tensors are ignored when window_tokens <= 0."""
-    b, two_t, h, d = k_Bx2TxHxD.shape
+    [B, H, Sr, D] with lengths [B, H]. The ring tensors are ignored when window_tokens <= 0.
+
+    One call per layer at the prefill -> decode switch, so the host work is kept short: every shape
+    and stride is read once, and the stride arrays handed to the library are cached by value."""
+    kshape = tuple(k_Bx2TxHxD.shape)
+    b, two_t, h, d = kshape
     t = two_t // 2
-    assert two_t == 2 * t and v_Bx2TxHxD.shape == k_Bx2TxHxD.shape
-    assert current_doc_mask_BxT.shape == (b, t), f"mask {tuple(current_doc_mask_BxT.shape)} vs ({b}, {t})"
-    assert br_k.shape[:2] == (b, h) and br_k.shape[3] == d and br_v.shape == br_k.shape
-    assert br_len.shape == (b, h)
+    assert two_t == 2 * t and tuple(v_Bx2TxHxD.shape) == kshape
+    mshape = tuple(current_doc_mask_BxT.shape)
+    assert mshape == (b, t), f"mask {mshape} vs ({b}, {t})"
+    rshape = tuple(br_k.shape)
+    assert rshape[:2] == (b, h) and rshape[3] == d and tuple(br_v.shape) == rshape
+    assert tuple(br_len.shape) == (b, h)
     window_tokens = int(window_tokens)
     use_ring = window_tokens > 0
     if use_ring:
-        assert nw_k.shape[:2] == (b, h) and nw_k.shape[3] == d and nw_v.shape == nw_k.shape
-        assert nw_len.shape == (b,) and nw_pos.shape == (b,)
-        assert window_tokens <= nw_k.size(2), "window_tokens exceeds the ring storage"
-    assert k_Bx2TxHxD.dtype in _FLOAT_DTYPES and v_Bx2TxHxD.dtype == k_Bx2TxHxD.dtype
-    assert br_k.dtype in _FLOAT_DTYPES and (not use_ring or nw_k.dtype == br_k.dtype)
-    assert br_len.dtype in _LEN_DTYPES and (not use_ring or (nw_len.dtype == br_len.dtype and nw_pos.dtype == br_len.dtype))
+        wshape = tuple(nw_k.shape)
+        assert wshape[:2] == (b, h) and wshape[3] == d and tuple(nw_v.shape) == wshape
+        assert tuple(nw_len.shape) == (b,) and tuple(nw_pos.shape) == (b,)
+        assert window_tokens <= wshape[2], "window_tokens exceeds the ring storage"
+    kdt, cdt, ldt = k_Bx2TxHxD.dtype, br_k.dtype, br_len.dtype
+    assert kdt in _FLOAT_DTYPES and v_Bx2TxHxD.dtype == kdt
+    assert cdt in _FLOAT_DTYPES and (not use_ring or nw_k.dtype == cdt)
+    assert ldt in _LEN_DTYPES and (not use_ring or (nw_len.dtype == ldt and nw_pos.dtype == ldt))
     assert d % 8 == 0, f"head_dim {d} must be a multiple of 8"
     assert k_Bx2TxHxD.is_cuda and br_k.is_cuda, "prefill_to_decode: tensors must be on the GPU"
     # The reference's slice assignment fails when a document does not fit the retained buffer. A
     # document has at most T tokens, so with a buffer of T rows or more this is a shape check; only a
     # shorter buffer needs the lengths read back (a host sync).
-    if b and br_k.size(2) < t:
+    if b and rshape[2] < t:
         longest = int(current_doc_mask_BxT.sum(dim=1).max())
-        if longest > br_k.size(2):
+        if longest > rshape[2]:
             raise RuntimeError(f"a prompt document of {longest} tokens does not fit the retained buffer "
-                               f"({br_k.size(2)} rows)")
-    k = k_Bx2TxHxD if _aligned(k_Bx2TxHxD) else k_Bx2TxHxD.contiguous()
-    v = v_Bx2TxHxD if _aligned(v_Bx2TxHxD) else v_Bx2TxHxD.contiguous()
-    for c in (br_k, br_v) + ((nw_k, nw_v) if use_ring else ()):
-        assert _aligned(c), "KV caches must have 16-byte aligned rows"
-    # A bool mask with unit column stride is read in place (one byte per flag, 0 or 1).
-    if current_doc_mask_BxT.dtype == torch.bool and current_doc_mask_BxT.stride(1) == 1:
-        mask = current_doc_mask_BxT.view(torch.uint8)
-    else:
-        mask = current_doc_mask_BxT.to(torch.uint8).contiguous()
-    cs = lambda x, y: N.i64_array((x.stride(0), x.stride(1), x.stride(2), y.stride(0), y.stride(1), y.stride(2)))  # noqa: E731
+                               f"({rshape[2]} rows)")
+    el_in, el_c = k_Bx2TxHxD.element_size(), br_k.element_size()
+    k, v = k_Bx2TxHxD, v_Bx2TxHxD
+    ks, vs = k.stride(), v.stride()
+    if not _rows16(k.data_ptr(), ks, el_in):
+        k = k.contiguous()
+        ks = k.stride()
+    if not _rows16(v.data_ptr(), vs, el_in):
+        v = v.contiguous()
+        vs = v.stride()
+    rk, rv = br_k.stride(), br_v.stride()
+    caches = [(br_k.data_ptr(), rk), (br_v.data_ptr(), rv)]
     if use_ring:
-        ring = (nw_k.data_ptr(), nw_v.data_ptr(), cs(nw_k, nw_v), nw_k.size(2), window_tokens, nw_len.data_ptr(),
-                nw_pos.data_ptr(), N.i64_array((nw_len.stride(0), nw_pos.stride(0))))
+        wk, wv = nw_k.stride(), nw_v.stride()
+        caches += [(nw_k.data_ptr(), wk), (nw_v.data_ptr(), wv)]
+    for ptr, st in caches:
+        assert _rows16(ptr, st, el_c), "KV caches must have 16-byte aligned rows"
+    # A bool mask with unit column stride is read in place (one byte per flag, 0 or 1).
+    mask = current_doc_mask_BxT
+    if mask.dtype == torch.bool and mask.stride(1) == 1:
+        mask = mask.view(torch.uint8)
     else:
-        ring = (None, None, N.i64_array((0,) * 6), 0, 0, None, None, N.i64_array((0, 0)))
+        mask = mask.to(torch.uint8).contiguous()
+    if use_ring:
+        ring = (caches[2][0], caches[3][0], N.i64_const(wk[:3] + wv[:3]), wshape[2], window_tokens,
+                nw_len.data_ptr(), nw_pos.data_ptr(), N.i64_const((nw_len.stride(0), nw_pos.stride(0))))
+    else:
+        ring = (None, None, N.i64_const((0,) * 6), 0, 0, None, None, N.i64_const((0, 0)))
     status = N.lib().sps_prefill_to_decode(
-        b, t, h, d, _FLOAT_DTYPES[k.dtype], k.data_ptr(), N.i64_array((k.stride(0), k.stride(1), k.stride(2))),
-        v.data_ptr(), N.i64_array((v.stride(0), v.stride(1), v.stride(2))), int(window_slot), int(retained_slot),
-        mask.data_ptr(), mask.stride(0), _FLOAT_DTYPES[br_k.dtype], *ring,
-        br_k.data_ptr(), br_v.data_ptr(), cs(br_k, br_v), br_k.size(2), br_len.data_ptr(),
-        N.i64_array((br_len.stride(0), br_len.stride(1))), _LEN_DTYPES[br_len.dtype],
-        torch.cuda.current_stream(k.device).cuda_stream)
+        b, t, h, d, _FLOAT_DTYPES[kdt], k.data_ptr(), N.i64_const(ks[:3]), v.data_ptr(), N.i64_const(vs[:3]),
+        int(window_slot), int(retained_slot), mask.data_ptr(), mask.stride(0), _FLOAT_DTYPES[cdt], *ring,
+        caches[0][0], caches[1][0], N.i64_const(rk[:3] + rv[:3]), rshape[2], br_len.data_ptr(),
+        N.i64_const(tuple(br_len.stride())), _LEN_DTYPES[ldt], torch.cuda.current_stream(k.device).cuda_stream)
     N.check("sps_prefill_to_decode", status)
 
 

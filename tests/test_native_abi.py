@@ -118,6 +118,15 @@ def test_last_error_truncates():
     assert full > 7 and len(buf.value) == 7
 
 
+def test_cached_stride_arrays():
+    a = N.i64_const((3, 5, 7))
+    assert list(a) == [3, 5, 7] and N.i64_const((3, 5, 7)) is a
+    assert list(N.i64_const((3, 5, 8))) == [3, 5, 8]
+    for i in range(1100):  # past the cache bound: emptied and refilled, values still right
+        assert N.i64_const((i, -i))[1] == -i
+    assert list(N.i64_const((3, 5, 7))) == [3, 5, 7]
+
+
 @cpu_only
 def test_backward_pass_selector_validation():
     lib = N.lib()
