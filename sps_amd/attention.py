@@ -15,6 +15,7 @@ no padding of N to a multiple of 128 (the kernels bounds-check), no ``.contiguou
 
 from __future__ import annotations
 
+import functools
 from typing import Optional, Tuple
 
 import torch
@@ -34,17 +35,14 @@ def _dtype_code(t: torch.Tensor) -> int:
 
 
 def _kernel_view(t: torch.Tensor) -> torch.Tensor:
-    """Returns t if the kernels can read it in place (unit d stride, 16-byte aligned rows)."""
-    ok = (
-        t.stride(3) == 1
-        and t.data_ptr() % 16 == 0
-        and all(s % 8 == 0 for s in (t.stride(0), t.stride(1), t.stride(2)))
-    )
-    return t if ok else t.contiguous()
+    """Returns t if the kernels can read it in place (unit d stride, 16-byte aligned rows: base and the
+    three outer strides, in 16-bit elements multiples of 8, tested at once on their OR)."""
+    s0, s1, s2, s3 = t.stride()
+    return t if (s3 == 1 and t.data_ptr() % 16 == 0 and (s0 | s1 | s2) % 8 == 0) else t.contiguous()
 
 
 def _strides(t: torch.Tensor):
-    return N.i64_array((t.stride(0), t.stride(1), t.stride(2)))
+    return N.i64_const(t.stride()[:3])
 
 
 def _docs_args(docs: Optional[torch.Tensor]):
@@ -68,9 +66,20 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-def _workspace(family: int, b: int, h: int, n: int, has_docs: bool, backward: bool, device) -> torch.Tensor:
-    nbytes = N.lib().sps_attn_workspace_bytes(family, b, h, n, int(has_docs), int(backward))
-    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+@functools.lru_cache(maxsize=256)
+def _workspace_bytes(family: int, b: int, h: int, n: int, has_docs: bool, backward: bool) -> int:
+    return int(N.lib().sps_attn_workspace_bytes(family, b, h, n, int(has_docs), int(backward)))
+
+
+def _workspace(family: int, b: int, h: int, n: int, has_docs: bool, backward: bool, device) -> Optional[torch.Tensor]:
+    """The call's workspace, or None when it needs none (the entry points take a null pointer then:
+    the forward without documents)."""
+    nbytes = _workspace_bytes(family, b, h, n, bool(has_docs), bool(backward))
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
+def _ws_args(ws: Optional[torch.Tensor]):
+    return (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
 
 
 def _validate(q, k, v, family, documents_idx_BxT):
@@ -115,7 +124,7 @@ def attention_forward(q, k, v, sm_scale, family, window=0, documents_idx_BxT=Non
         o.data_ptr(), _strides(o), lse.data_ptr(),
         docs_ptr, docs_code, docs_sb,
         float(sm_scale), int(window), int(has_pkw), int(persistent_key_window) if has_pkw else -1,
-        ws.data_ptr(), ws.numel(), _stream(q),
+        *_ws_args(ws), _stream(q),
     )
     N.check("sps_attn_fwd", status)
     return o, lse, q, k, v, (ws if keep else None)
@@ -137,7 +146,7 @@ def backward_pass_args(do, q, k, v, o, lse, dq, dk, dv, sm_scale, family, window
         dq.data_ptr(), _strides(dq), dk.data_ptr(), _strides(dk), dv.data_ptr(), _strides(dv),
         docs_ptr, docs_code, docs_sb,
         float(sm_scale), int(window), int(has_pkw), int(persistent_key_window) if has_pkw else -1,
-        ws.data_ptr(), ws.numel(), _stream(q),
+        *_ws_args(ws), _stream(q),
     ), ws
 
 
@@ -312,7 +321,7 @@ def attention_mask(family: int, n: int, documents_idx_BxT: Optional[torch.Tensor
     status = N.lib().sps_attn_mask(
         family, batch, n, docs_ptr, docs_code, docs_sb, int(window), int(has_pkw),
         int(persistent_key_window) if has_pkw else -1, int(schedule), mask.data_ptr(),
-        ws.data_ptr(), ws.numel(), torch.cuda.current_stream(device).cuda_stream,
+        *_ws_args(ws), torch.cuda.current_stream(device).cuda_stream,
     )
     N.check("sps_attn_mask", status)
     return mask
