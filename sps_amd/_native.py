@@ -199,19 +199,36 @@ def i64_array(values) -> C.Array:
     return (C.c_int64 * max(len(vals), 1))(*vals)
 
 
-_I64_CACHE: dict = {}
+_CONST_CACHE: dict = {}
+
+
+def _const_array(ctype, values: tuple) -> C.Array:
+    """A ctypes array of `values`, cached by value, for the array arguments of per-call host paths
+    (strides, sizes, pointers that stay the same from call to call, such as KV caches): the native
+    entry points only read these arrays during the call and nothing writes them, so equal tuples can
+    share one array (the cache is emptied past 1024 entries)."""
+    key = (ctype, values)
+    arr = _CONST_CACHE.get(key)
+    if arr is None:
+        if len(_CONST_CACHE) >= 1024:
+            _CONST_CACHE.clear()
+        arr = _CONST_CACHE[key] = (ctype * max(len(values), 1))(*values)
+    return arr
 
 
 def i64_const(values: tuple) -> C.Array:
-    """i64_array of a tuple of ints, cached by value, for stride and size arguments of per-call host
-    paths: the native entry points only read these arrays during the call and nothing writes them,
-    so equal tuples can share one array (the cache is emptied past 1024 entries)."""
-    arr = _I64_CACHE.get(values)
-    if arr is None:
-        if len(_I64_CACHE) >= 1024:
-            _I64_CACHE.clear()
-        arr = _I64_CACHE[values] = i64_array(values)
-    return arr
+    """i64_array of a tuple of ints, cached by value (see _const_array)."""
+    return _const_array(C.c_int64, values)
+
+
+def i32_const(values: tuple) -> C.Array:
+    """i32_array of a tuple of ints, cached by value (see _const_array)."""
+    return _const_array(C.c_int, values)
+
+
+def ptr_const(values: tuple) -> C.Array:
+    """ptr_array of a tuple of addresses (ints or None for null), cached by value (see _const_array)."""
+    return _const_array(C.c_void_p, values)
 
 
 def i32_array(values) -> C.Array:

@@ -14,6 +14,7 @@ HIP kernels of libsps_attn.so. There is no CPU path: ``masked_kv_attention`` on 
 
 from __future__ import annotations
 
+import functools
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -69,39 +70,49 @@ def _as_attn(t: Tensor, attn_dtype: torch.dtype) -> Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+@functools.lru_cache(maxsize=256)
+def _decode_ws_bytes(fused_update: bool, b: int, h: int, d: int, nq: int, kv_dtype: int, scans: tuple) -> int:
+    lib = N.lib()
+    fn = lib.sps_decode_kv_update_workspace_bytes if fused_update else lib.sps_decode_workspace_bytes
+    return int(fn(b, h, d, nq, kv_dtype, len(scans), N.i64_const(scans)))
+
+
 def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor, static_scratch: bool = False,
                 kv_update: Optional[tuple] = None) -> Tensor:
     """Calls sps_decode. q: [B, nq, H, D] (bf16/f16/f32); extras: list of (k, v) [B, H, D] sharing one
     dtype and one (b, h) stride pair. ``static_scratch`` calls sps_decode_static instead, which keeps
     its partial records in the library's own scratch array (no workspace is allocated). ``kv_update``
     (the argument tuple of decode_attention_fast.kv_update_args) calls sps_decode_kv_update instead:
-    the same attention, then that KV update of the caches, in the attention's launches."""
+    the same attention, then that KV update of the caches, in the attention's launches.
+
+    One call per layer and generated token, so the host work is kept short: the workspace sizes are
+    memoized per shape, and the array arguments, which repeat from step to step (the caches and their
+    strides stay put), are cached by value."""
     b, _, h, d = q.shape
-    kv_dtype = N.DTYPE_BF16
-    if segments:
-        kv_dtype = _KV_DTYPES[segments[0].k.dtype]
-    scans = [_segment_scan_len(s) for s in segments]
-    lens = [s.lengths.contiguous() for s in segments]
+    kv_dtype = _KV_DTYPES[segments[0].k.dtype] if segments else N.DTYPE_BF16
+    scans = tuple(_segment_scan_len(sg) for sg in segments)
+    lens = [sg.lengths.contiguous() for sg in segments]
     lib = N.lib()
-    scan_arr = N.i64_array(scans)
     ws = None
     if kv_update is not None:
         upd = kv_update[0]
         if segments and upd[3] != kv_dtype:
             raise RuntimeError("decode with KV update: the caches must have the segments' dtype")
-        ws_bytes = lib.sps_decode_kv_update_workspace_bytes(b, h, d, nq, kv_dtype, len(segments), scan_arr)
-        ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
+        ws = torch.empty(max(_decode_ws_bytes(True, b, h, d, nq, kv_dtype, scans), 1), dtype=torch.uint8,
+                         device=q.device)
     elif not static_scratch:
-        ws_bytes = lib.sps_decode_workspace_bytes(b, h, d, nq, kv_dtype, len(segments), scan_arr)
-        ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=q.device)
-    k_strides, v_strides = [], []
-    for s in segments:
-        k_strides += [s.k.stride(0), s.k.stride(1), s.k.stride(2)]
-        v_strides += [s.v.stride(0), s.v.stride(1), s.v.stride(2)]
-    ek = [e[0] for e in extras]
-    ev = [e[1] for e in extras]
-    e_strides = (ek[0].stride(0), ek[0].stride(1)) if extras else (0, 0)
-    e_dtype = _KV_DTYPES[ek[0].dtype] if extras else N.DTYPE_F32
+        ws = torch.empty(max(_decode_ws_bytes(False, b, h, d, nq, kv_dtype, scans), 1), dtype=torch.uint8,
+                         device=q.device)
+    k_strides = tuple(x for sg in segments for x in sg.k.stride()[:3])
+    v_strides = tuple(x for sg in segments for x in sg.v.stride()[:3])
+    if extras:
+        ek = tuple(e[0].data_ptr() for e in extras)
+        ev = tuple(e[1].data_ptr() for e in extras)
+        e_strides = extras[0][0].stride()[:2]
+        e_dtype = _KV_DTYPES[extras[0][0].dtype]
+    else:
+        ek = ev = ()
+        e_strides, e_dtype = (0, 0), N.DTYPE_F32
     if kv_update is not None:
         name, entry, tail = "sps_decode_kv_update", lib.sps_decode_kv_update, (*kv_update[0][4:-1], ws.data_ptr(),
                                                                                 ws.numel())
@@ -111,15 +122,15 @@ def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor, 
         name, entry, tail = "sps_decode", lib.sps_decode, (ws.data_ptr(), ws.numel())
     status = entry(
         b, h, d, nq,
-        q.data_ptr(), _KV_DTYPES[q.dtype], N.i64_array((q.stride(0), q.stride(1), q.stride(2))),
+        q.data_ptr(), _KV_DTYPES[q.dtype], N.i64_const(q.stride()[:3]),
         kv_dtype, len(segments),
-        N.ptr_array([s.k.data_ptr() for s in segments]), N.i64_array(k_strides),
-        N.ptr_array([s.v.data_ptr() for s in segments]), N.i64_array(v_strides),
-        N.ptr_array([ln.data_ptr() for ln in lens]), N.i32_array([_len_dtype(ln) for ln in lens]),
-        N.i32_array([int(ln.dim() == 2) for ln in lens]), scan_arr,
-        len(extras), N.ptr_array([t.data_ptr() for t in ek]), N.ptr_array([t.data_ptr() for t in ev]), e_dtype,
-        N.i64_array(e_strides), N.i32_array(extra_masks),
-        1.0 / math.sqrt(d), out.data_ptr(), N.i64_array((out.stride(0), out.stride(1), out.stride(2))),
+        N.ptr_const(tuple(sg.k.data_ptr() for sg in segments)), N.i64_const(k_strides),
+        N.ptr_const(tuple(sg.v.data_ptr() for sg in segments)), N.i64_const(v_strides),
+        N.ptr_const(tuple(ln.data_ptr() for ln in lens)), N.i32_const(tuple(_len_dtype(ln) for ln in lens)),
+        N.i32_const(tuple(int(ln.dim() == 2) for ln in lens)), N.i64_const(scans),
+        len(extras), N.ptr_const(ek), N.ptr_const(ev), e_dtype,
+        N.i64_const(tuple(e_strides)), N.i32_const(tuple(extra_masks)),
+        1.0 / math.sqrt(d), out.data_ptr(), N.i64_const(out.stride()[:3]),
         *tail, torch.cuda.current_stream(q.device).cuda_stream,
     )
     N.check(name, status)
@@ -128,37 +139,47 @@ def _run_decode(q: Tensor, nq: int, segments, extras, extra_masks, out: Tensor, 
 
 def _extras_in(extra_kv, attn_dtype, b, h, d):
     """Extra (k, v) pairs in the attention dtype with one shared (b, h) stride pair."""
-    out = [(_as_attn(ek, attn_dtype).expand(b, h, d), _as_attn(ev, attn_dtype).expand(b, h, d))
-           for ek, ev in extra_kv]
-    if len({(k.stride(0), k.stride(1)) for pair in out for k in pair}) > 1:
+    shape = (b, h, d)
+
+    def conv(t):
+        t = _as_attn(t, attn_dtype)
+        return t if t.shape == shape else t.expand(b, h, d)
+
+    out = [(conv(ek), conv(ev)) for ek, ev in extra_kv]
+    if len({k.stride()[:2] for pair in out for k in pair}) > 1:
         out = [(k.contiguous(), v.contiguous()) for k, v in out]
     return out
 
 
 def _segments_compatible(segments, batch_size, n_head, head_dim, device) -> bool:
-    dtypes = {s.k.dtype for s in segments} | {s.v.dtype for s in segments}
-    if len(dtypes) > 1 or (dtypes and next(iter(dtypes)) not in _KV_DTYPES):
-        return False
+    dtype = None
     for seg in segments:
-        if seg.k.dim() != 4 or seg.v.dim() != 4 or seg.k.shape != seg.v.shape:
+        k, v, ln = seg.k, seg.v, seg.lengths
+        if dtype is None:
+            dtype = k.dtype
+        if k.dtype != dtype or v.dtype != dtype:
             return False
-        if seg.k.size(0) != batch_size or seg.k.size(1) != n_head or seg.k.size(3) != head_dim:
+        kshape = k.shape
+        if len(kshape) != 4 or v.shape != kshape:
             return False
-        if seg.lengths.device != device or seg.lengths.dim() not in (1, 2):
+        if kshape[0] != batch_size or kshape[1] != n_head or kshape[3] != head_dim:
             return False
-        if seg.lengths.dtype not in (torch.int32, torch.int64):
+        if ln.device != device or ln.dtype not in (torch.int32, torch.int64):
             return False
-        if seg.lengths.dim() == 2 and tuple(seg.lengths.shape) != (batch_size, n_head):
-            return False
-        if seg.lengths.dim() == 1 and seg.lengths.shape[0] != batch_size:
-            return False
-        esize = seg.k.element_size()
-        for t in (seg.k, seg.v):
-            if t.stride(3) != 1 or t.data_ptr() % 16 != 0:
+        ldim = ln.dim()
+        if ldim == 2:
+            if tuple(ln.shape) != (batch_size, n_head):
                 return False
-            if any((s * esize) % 16 != 0 for s in (t.stride(0), t.stride(1), t.stride(2))):
+        elif ldim != 1 or ln.shape[0] != batch_size:
+            return False
+        # Unit d stride and 16-byte aligned rows (power-of-two element sizes: one test of the three
+        # outer strides' OR covers all three).
+        esize = k.element_size()
+        for t in (k, v):
+            s0, s1, s2, s3 = t.stride()
+            if s3 != 1 or t.data_ptr() % 16 != 0 or ((s0 | s1 | s2) * esize) % 16 != 0:
                 return False
-    return True
+    return dtype is None or dtype in _KV_DTYPES
 
 
 def triton_segmented_q1_attention(
@@ -184,10 +205,9 @@ def triton_segmented_q1_attention(
     batch_size, n_head, head_dim = q_BxHxD.shape
     if head_dim not in _DECODE_HEAD_DIMS:
         return None
-    if any((not seg.k.is_cuda) or (not seg.v.is_cuda) for seg in segments):
-        return None
-    if any((not seg.k.is_contiguous()) or (not seg.v.is_contiguous()) for seg in segments):
-        return None
+    for seg in segments:
+        if not (seg.k.is_cuda and seg.v.is_cuda and seg.k.is_contiguous() and seg.v.is_contiguous()):
+            return None
     if not _segments_compatible(segments, batch_size, n_head, head_dim, q_BxHxD.device):
         return None
     if attn_dtype not in _KV_DTYPES:

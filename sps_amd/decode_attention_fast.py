@@ -33,13 +33,15 @@ _FLAG_DTYPES = {torch.bool: N.DTYPE_U8, torch.uint8: N.DTYPE_U8, torch.int8: N.D
 
 
 def _cache_strides(t: Tensor):
-    assert t.dim() == 4 and t.stride(3) == 1, "KV caches must be [B, H, storage, D] with a contiguous D axis"
-    return t.stride(0), t.stride(1), t.stride(2)
+    st = t.stride()
+    assert len(st) == 4 and st[3] == 1, "KV caches must be [B, H, storage, D] with a contiguous D axis"
+    return st[:3]
 
 
 def _new_strides(t: Tensor):
-    assert t.dim() == 3 and t.stride(2) == 1, "new K/V must be [B, H, D] with a contiguous D axis"
-    return t.stride(0), t.stride(1)
+    st = t.stride()
+    assert len(st) == 3 and st[2] == 1, "new K/V must be [B, H, D] with a contiguous D axis"
+    return st[:2]
 
 
 def kv_update_args(
@@ -96,16 +98,16 @@ def kv_update_args(
     ret_st = _cache_strides(br_k) + _cache_strides(br_v)
     if use_ring:
         ring_st = _cache_strides(nw_k) + _cache_strides(nw_v)
-        ring = (nw_k.data_ptr(), nw_v.data_ptr(), N.i64_array(ring_st), nw_k.size(2), window_tokens,
-                nw_len.data_ptr(), nw_pos.data_ptr(), N.i64_array((nw_len.stride(0), nw_pos.stride(0))))
+        ring = (nw_k.data_ptr(), nw_v.data_ptr(), N.i64_const(ring_st), nw_k.size(2), window_tokens,
+                nw_len.data_ptr(), nw_pos.data_ptr(), N.i64_const((nw_len.stride(0), nw_pos.stride(0))))
     else:
-        ring = (None, None, N.i64_array((0,) * 6), 0, 0, None, None, N.i64_array((0, 0)))
+        ring = (None, None, N.i64_const((0,) * 6), 0, 0, None, None, N.i64_const((0, 0)))
     args = (
         batch_size, n_head, head_dim, _FLOAT_DTYPES[br_k.dtype],
         *ring,
-        br_k.data_ptr(), br_v.data_ptr(), N.i64_array(ret_st), br_k.size(2),
-        br_len.data_ptr(), N.i64_array((br_len.stride(0), br_len.stride(1))), _LEN_DTYPES[br_len.dtype],
-        _FLOAT_DTYPES[new_dtype], kw.data_ptr(), vw.data_ptr(), kr.data_ptr(), vr.data_ptr(), N.i64_array(ns),
+        br_k.data_ptr(), br_v.data_ptr(), N.i64_const(ret_st), br_k.size(2),
+        br_len.data_ptr(), N.i64_const(tuple(br_len.stride())), _LEN_DTYPES[br_len.dtype],
+        _FLOAT_DTYPES[new_dtype], kw.data_ptr(), vw.data_ptr(), kr.data_ptr(), vr.data_ptr(), N.i64_const(ns),
         active_mask_B.data_ptr(), _FLAG_DTYPES[active_mask_B.dtype], active_mask_B.stride(0),
         torch.cuda.current_stream(br_k.device).cuda_stream,
     )
