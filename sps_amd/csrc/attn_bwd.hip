@@ -195,19 +195,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(dq_waves<D>
 
   if (planned) q_lanes(m, qp, run_start, st);
 
-  // Delta = rowsum(O * dO) of the lane's query, stored for the dK/dV pass.
+  // Delta = rowsum(O * dO) of the lane's query, stored for the dK/dV pass: one v_dot2 per packed pair
+  // (two exact products and the fp32 accumulation in one instruction), two independent partial sums.
   float delta;
   {
-    float part = 0.f;
+    float part[2] = {0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        part += E::to_f32((uint16_t)(of[c][j] & 0xffffu)) * E::to_f32((uint16_t)(dof[c][j] & 0xffffu));
-        part += E::to_f32((uint16_t)(of[c][j] >> 16)) * E::to_f32((uint16_t)(dof[c][j] >> 16));
-      }
+      for (int j = 0; j < 4; ++j) part[j & 1] = E::dot2(of[c][j], dof[c][j], part[j & 1]);
     }
-    delta = half_sum(part);
+    delta = half_sum(part[0] + part[1]);
   }
   const float lse = lse_raw == -INFINITY ? 0.f : lse_raw;  // a query with no visible key: every score is masked to -inf
   if (qvalid && g == 0) {

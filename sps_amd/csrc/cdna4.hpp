@@ -54,6 +54,11 @@ struct ElemBF16 {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pair), __builtin_bit_cast(bf16x2_t, ones),
                                           acc, false);
   }
+  // acc + a.lo * b.lo + a.hi * b.hi of two packed pairs (v_dot2_f32_bf16; the products are exact in fp32).
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc,
+                                          false);
+  }
 };
 
 struct ElemF16 {
@@ -72,6 +77,10 @@ struct ElemF16 {
   static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
     const uint32_t ones = 0x3c003c00u;
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, pair), __builtin_bit_cast(f16x2_t, ones), acc, false);
+  }
+  // acc + a.lo * b.lo + a.hi * b.hi of two packed pairs (v_dot2_f32_f16; the products are exact in fp32).
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), acc, false);
   }
 };
 
