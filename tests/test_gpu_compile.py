@@ -108,3 +108,52 @@ def test_compiled_block_through_the_installed_rope_matches_eager(monkeypatch):
         results.append([loss.detach()] + [p.grad.clone() for p in (*c_attn.parameters(), *c_proj.parameters())])
     for got, want in zip(results[1], results[0]):
         torch.testing.assert_close(got, want, atol=0, rtol=0)
+
+
+def test_inductor_compiled_block_matches_eager(monkeypatch):
+    # The same attention-module forward under the default torch.compile backend (inductor), as the
+    # reference trains: the surrounding projection, casts and loss are compiled by inductor, the RoPE
+    # and attention stay the library's custom ops (extern calls in the compiled graph). Fused
+    # elementwise work and reductions may round differently from eager, so the comparison has a
+    # tolerance; the attention itself sees the same inputs either way.
+    import sys
+    import types
+
+    model_mod = types.ModuleType("modeling.models.model")
+    model_mod.apply_rotary_emb = _reference_apply_rotary_emb
+    monkeypatch.setitem(sys.modules, "modeling.models.model", model_mod)
+    sps_amd.install_into_modeling()
+    torch._dynamo.reset()
+
+    b, two_t, h, d, w = 2, 256, 4, 64, 16
+    c = h * d
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((b, two_t, c), generator=g).cuda()
+    inv = 1.0 / (10000.0 ** (torch.arange(0, d, 2).float() / d))
+    freqs = torch.polar(torch.ones(two_t, d // 2), torch.outer(torch.arange(two_t).float(), inv)).cuda()
+    docs = torch.tensor(np.repeat(np.array([[0] * 60 + [1] * 68] * b), 2, axis=1), device="cuda")
+    torch.manual_seed(0)
+    c_attn, c_proj = torch.nn.Linear(c, 3 * c).cuda(), torch.nn.Linear(c, c).cuda()
+
+    def block(x):
+        from modeling.models.model import apply_rotary_emb
+
+        q, k, v = c_attn(x).split(c, dim=2)
+        q, k = q.view(b, two_t, h, d), k.view(b, two_t, h, d)
+        v = v.view(b, two_t, h, d).transpose(1, 2)
+        q, k = apply_rotary_emb(q, k, freqs_cis=freqs)
+        q, k, v = q.transpose(1, 2).to(torch.bfloat16), k.transpose(1, 2).to(torch.bfloat16), v.to(torch.bfloat16)
+        y = sps_amd.sps_sliding_attention(q, k, v, 1 / math.sqrt(d), w, documents_idx_BxT=docs)
+        y = y.transpose(1, 2).contiguous().view(b, two_t, c).to(c_proj.weight.dtype)
+        return c_proj(y).square().mean()
+
+    results = []
+    for fn in (block, torch.compile(block, fullgraph=True)):
+        for p in (*c_attn.parameters(), *c_proj.parameters()):
+            p.grad = None
+        loss = fn(x)
+        loss.backward()
+        torch.cuda.synchronize()
+        results.append([loss.detach()] + [p.grad.clone() for p in (*c_attn.parameters(), *c_proj.parameters())])
+    for got, want in zip(results[1], results[0]):
+        torch.testing.assert_close(got, want, atol=1e-4, rtol=2e-2)
