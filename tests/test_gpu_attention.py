@@ -70,6 +70,28 @@ def _check(family, b, h, n, d, window=0, docs=None, pkw=None, dtype=torch.bfloat
                                        msg=lambda m, name=name: f"{name}: {m}")
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_parity_random_sweep(seed):
+    # Outputs and gradients at random small configurations against the float64 oracle, to the same
+    # bound as the fixed matrix: each family with a random length, head dim, window, persistent-key
+    # window, document layout (none, packed runs, non-monotone random ids), dtype and memory layout.
+    rng = np.random.default_rng(2000 + seed)
+    for family in ("full", "sps", "reverse_sps"):
+        n = int(rng.integers(1, 401)) if family == "full" else 2 * int(rng.integers(1, 201))
+        d = int(rng.choice([16, 32, 64, 64, 128, 256]))
+        b, h = int(rng.integers(1, 3)), int(rng.integers(1, 3))
+        window = int(rng.choice([-1, 0, 3, 64, n, int(rng.integers(0, n + 1))])) if family != "full" else 0
+        pkw = int(rng.choice([0, 1, int(rng.integers(0, n + 1))])) if family != "full" and rng.random() < 0.5 else None
+        tokens = n if family == "full" else n // 2
+        kind = int(rng.integers(3))
+        docs = (None if kind == 0 else _packed_docs(rng, b, tokens, family, max_len=int(rng.integers(2, max(3, tokens + 1))))
+                if kind == 1 else rng.integers(0, 3, size=(b, n)).astype(np.int64))
+        dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+        layout = "bhnd" if rng.random() < 0.5 else "bnhd"
+        _check(family, b, h, n, d, window=window, docs=docs, pkw=pkw, dtype=dtype, seed=int(rng.integers(1 << 30)),
+               layout=layout)
+
+
 @pytest.mark.parametrize("family", ["sps", "reverse_sps"])
 @pytest.mark.parametrize("has_docs", [False, True])
 def test_reference_kernel_test_shape(family, has_docs):
@@ -199,6 +221,45 @@ def test_mask_bit_exact(case, schedule):
                             schedule=schedule).cpu().numpy().astype(bool)
     want = M.batch_mask(FAMILY[family], docs, n=n, window=w, pkw=pkw, batch=b)
     assert (got == want).all(), f"{int((got != want).sum())} mismatching pairs"
+
+
+def _random_mask_case(rng):
+    family = ("full", "sps", "reverse_sps")[int(rng.integers(3))]
+    n = int(rng.integers(1, 701)) if family == "full" else 2 * int(rng.integers(1, 351))
+    b = int(rng.integers(1, 4))
+    window = int(rng.choice([-1, 0, 1, 2, n, n + 5, int(rng.integers(0, n + 1))]))
+    pkw = None
+    if family != "full" and rng.random() < 0.4:
+        pkw = int(rng.choice([-1, 0, 1, int(rng.integers(0, n + 1))]))
+    tokens = n if family == "full" else n // 2
+    kind = int(rng.integers(4))
+    if kind == 0:
+        docs = None
+    elif kind == 1:
+        docs = _packed_docs(rng, b, tokens, family, max_len=int(rng.integers(2, max(3, tokens + 1))))
+    elif kind == 2:
+        docs = rng.integers(0, int(rng.integers(1, 5)), size=(b, n)).astype(np.int64)
+    else:
+        docs = np.zeros((b, n), dtype=np.int64)
+    return family, n, b, window, pkw, docs
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_mask_random_sweep(seed):
+    # Random families, lengths (odd ones for full attention), batch sizes, windows (-1, 0, 1, 2, past
+    # the row, random), persistent-key windows and document layouts (none, packed runs down to length
+    # 1, non-monotone random ids, one document): the kernels' masks under both block schedules equal
+    # the oracle predicate on every pair.
+    rng = np.random.default_rng(1000 + seed)
+    for _ in range(8):
+        family, n, b, window, pkw, docs = _random_mask_case(rng)
+        docs_t = None if docs is None else torch.tensor(docs, device="cuda")
+        want = M.batch_mask(FAMILY[family], docs, n=n, window=window, pkw=pkw, batch=b)
+        for schedule in (0, 1):
+            got = SA.attention_mask(FAMILY[family], n, docs_t, batch=b, window=window, persistent_key_window=pkw,
+                                    schedule=schedule).cpu().numpy().astype(bool)
+            case = f"{family} n={n} b={b} w={window} pkw={pkw} docs={'none' if docs is None else docs[0, :12]}"
+            assert (got == want).all(), f"schedule {schedule}, {case}: {int((got != want).sum())} mismatching pairs"
 
 
 @pytest.mark.parametrize("family,n", [("sps", 4096), ("full", 4096), ("reverse_sps", 8320)])
