@@ -90,6 +90,60 @@ def test_q1_matches_oracle(case):
     torch.testing.assert_close(got.cpu(), torch.from_numpy(want).float(), atol=ATOL, rtol=RTOL)
 
 
+def _random_segments(rng, g, b, h, d, n_seg, dev):
+    kv_dtype = (torch.bfloat16, torch.float16, torch.float32)[int(rng.integers(3))]
+    len_dtype = torch.int64 if rng.random() < 0.7 else torch.int32
+    segments = []
+    for _ in range(n_seg):
+        storage = int(rng.choice([0, 1, 5, 64, int(rng.integers(1, 1200))]))
+        cap = (None, 0, 1, storage, storage + 9, int(rng.integers(0, max(storage, 1) + 1)))[int(rng.integers(6))]
+        shape = (b, h) if rng.random() < 0.5 else (b,)
+        lens = rng.integers(-3, storage + 4, size=shape) if storage else np.zeros(shape, dtype=np.int64)
+        k = torch.randn((b, h, storage, d), generator=g).to(kv_dtype).to(dev)
+        v = torch.randn((b, h, storage, d), generator=g).to(kv_dtype).to(dev)
+        segments.append(DA.KVSegment(k, v, torch.tensor(lens, dtype=len_dtype, device=dev), max_len_cap=cap))
+    return segments
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_decode_random_sweep(seed):
+    # q=1 and q=2 decode at random configurations against the oracle: batch, heads, head dim, 0-3
+    # segments (q=2: up to 2) of random storage, caps (none, 0, 1, the storage, past it, random),
+    # lengths from -3 to past the storage, per-head or shared, int32/int64, bf16/f16/fp32 K/V, bf16 or
+    # fp32 queries, 0-2 extra keys.
+    rng = np.random.default_rng(3000 + seed)
+    g = torch.Generator().manual_seed(seed)
+    dev = "cuda"
+    for _ in range(3):
+        b, h = int(rng.integers(1, 7)), int(rng.integers(1, 5))
+        d = int(rng.choice([16, 32, 64, 64, 128, 256]))
+        segments = _random_segments(rng, g, b, h, d, int(rng.integers(0, 4)), dev)
+        q_dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+        q = torch.randn((b, h, d), generator=g).to(q_dtype).to(dev)
+        n_extra = int(rng.integers(0, 3))
+        extras = [(torch.randn((b, h, d), generator=g).to(dev), torch.randn((b, h, d), generator=g).to(dev))
+                  for _ in range(n_extra)]
+        got = DA.triton_segmented_q1_attention(q, segments, extra_kv=extras or None, attn_dtype=torch.bfloat16)
+        assert got is not None
+        want = Dc.attend(_round(q, torch.bfloat16).reshape(b, 1, h, d), _np_segs(segments),
+                         [(_round(ek, torch.bfloat16), _round(ev, torch.bfloat16)) for ek, ev in extras],
+                         [1] * n_extra, 1)[:, 0]
+        torch.testing.assert_close(got.cpu(), torch.from_numpy(want).float(), atol=ATOL, rtol=RTOL)
+    for _ in range(2):
+        b, h = int(rng.integers(1, 7)), int(rng.integers(1, 5))
+        d = int(rng.choice([16, 32, 64, 64, 128, 256]))
+        segments = _random_segments(rng, g, b, h, d, int(rng.integers(0, 3)), dev)
+        q = torch.randn((b, 2, h, d), generator=g).to(torch.bfloat16).to(dev)
+        cur = [torch.randn((b, h, d), generator=g).to(torch.bfloat16).to(dev) for _ in range(4)]
+        got = DA.triton_segmented_q2_attention(
+            q, segments, current_normal_k_BxHxD=cur[0], current_normal_v_BxHxD=cur[1],
+            current_predict_k_BxHxD=cur[2], current_predict_v_BxHxD=cur[3], attn_dtype=torch.bfloat16)
+        want = Dc.attend(q.float().cpu().numpy(), _np_segs(segments),
+                         [(cur[0].float().cpu().numpy(), cur[1].float().cpu().numpy()),
+                          (cur[2].float().cpu().numpy(), cur[3].float().cpu().numpy())], [0b11, 0b10], 2)
+        torch.testing.assert_close(got.cpu(), torch.from_numpy(want).float(), atol=ATOL, rtol=RTOL)
+
+
 def test_c5_full_size_against_oracle():
     # C5: 64 sequences, 16 heads, D 64, retained lengths U[512, 4096] (seed 0), ring of 64 full,
     # one <predict> query (ring + retained + current input + current <predict>).
