@@ -134,6 +134,24 @@ def test_fused_step_equals_attention_then_update(nq, cache_dtype, new_dtype):
     _run_case(9, 5, 64, 8, 6, 700, cache_dtype, new_dtype, nq, steps=4, seed=11)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_random_sweep(seed):
+    # Random shapes, head dims, windows (0 = no ring), storages (including buffers that fill during the
+    # run), cache and new-K/V dtypes, length dtypes, q=1 / q=2 and active rates: the fused step equals
+    # the attention followed by the update, and the oracle's caches, every step.
+    rng = np.random.default_rng(5000 + seed)
+    dtypes = (torch.bfloat16, torch.float16, torch.float32)
+    for case in range(2):
+        window = int(rng.integers(0, 9))
+        cache_dtype = dtypes[int(rng.integers(3))]
+        new_dtype = cache_dtype if rng.random() < 0.7 else dtypes[int(rng.integers(3))]
+        _run_case(int(rng.integers(1, 10)), int(rng.integers(1, 6)), int(rng.choice([16, 32, 64, 128, 256])),
+                  window + int(rng.integers(0, 4)) if window else int(rng.integers(1, 4)), window,
+                  int(rng.integers(1, 400)), cache_dtype, new_dtype, int(rng.integers(1, 3)),
+                  steps=int(rng.integers(2, 6)), seed=int(rng.integers(1 << 30)),
+                  len_dtype=torch.long if rng.random() < 0.6 else torch.int32, active_p=float(rng.uniform(0.3, 1.0)))
+
+
 @pytest.mark.parametrize("D", [16, 32, 128, 256])
 def test_head_dims_and_int32_lengths(D):
     _run_case(5, 3, D, 4, 4, 300, torch.bfloat16, torch.bfloat16, 2, steps=3, seed=D, len_dtype=torch.int32)

@@ -99,6 +99,34 @@ def test_random_states_match_oracle(cache_dtype, new_dtype):
         st = {k: v.cpu() for k, v in st_gpu.items()}
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_random_sweep(seed):
+    # Random shapes, windows (0 = no ring), storages, cache and new-K/V dtypes, length dtypes, strided
+    # or contiguous caches and active flags, over several consecutive steps: bit-exact every step.
+    rng = np.random.default_rng(4000 + seed)
+    gen = torch.Generator().manual_seed(seed)
+    dtypes = (torch.bfloat16, torch.float16, torch.float32)
+    for case in range(3):
+        B, H = int(rng.integers(1, 10)), int(rng.integers(1, 6))
+        D = int(rng.choice([16, 64, 100, 128, 256]))
+        window = int(rng.integers(0, 8))
+        ring_storage = window + int(rng.integers(0, 4)) if window else int(rng.integers(1, 4))
+        ret_storage = int(rng.integers(1, 21))
+        cache_dtype, new_dtype = dtypes[int(rng.integers(3))], dtypes[int(rng.integers(3))]
+        len_dtype = torch.long if rng.random() < 0.6 else torch.int32
+        st = _make_state(B, H, D, ring_storage, max(window, 1), ret_storage, cache_dtype, len_dtype, gen,
+                         strided=bool(rng.random() < 0.4))
+        st_gpu = _to_gpu(st)
+        for step in range(int(rng.integers(3, 6))):
+            new = [torch.randn(B, H, D, generator=gen).to(new_dtype) for _ in range(4)]
+            active = torch.rand(B, generator=gen) < 0.75
+            ref = _oracle_step(st, new, active, window, cache_dtype)
+            _gpu_step(st_gpu, new, active, window)
+            torch.cuda.synchronize()
+            _check(st_gpu, ref, f"case {case} (B{B} H{H} D{D} w{window} {cache_dtype}<-{new_dtype}) step {step}")
+            st = {k: v.cpu() for k, v in st_gpu.items()}
+
+
 @pytest.mark.parametrize("D", [16, 100, 128, 256])
 def test_strided_caches_int32_lengths_int64_flags(D):
     gen = torch.Generator().manual_seed(D)

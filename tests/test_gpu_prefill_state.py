@@ -60,6 +60,29 @@ def test_trailing_documents(in_dtype, cache_dtype):
     _run(B, T, H, D, 8, in_dtype, cache_dtype, _trailing_docs(B, T, g), 1, 0, seed=2)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_random_sweep(seed):
+    # Random shapes, head dims, windows, dtypes, slot roles, length dtypes, strided or contiguous caches,
+    # and masks (trailing documents, arbitrary bits, all, none): bit-exact against the oracle.
+    rng = np.random.default_rng(6000 + seed)
+    dtypes = (torch.bfloat16, torch.float16, torch.float32)
+    for case in range(3):
+        B, T, H = int(rng.integers(1, 7)), int(rng.integers(1, 300)), int(rng.integers(1, 5))
+        D = int(rng.choice([16, 64, 128, 256]))
+        g = torch.Generator().manual_seed(int(rng.integers(1 << 30)))
+        kind = int(rng.integers(4))
+        if kind == 0:
+            mask = _trailing_docs(B, T, g)
+        elif kind == 1:
+            mask = torch.rand(B, T, generator=g) < float(rng.uniform(0.1, 0.9))
+        else:
+            mask = torch.full((B, T), kind == 2)
+        slot = int(rng.integers(2))
+        _run(B, T, H, D, int(rng.choice([0, 1, 5, 64, T + 3])), dtypes[int(rng.integers(3))],
+             dtypes[int(rng.integers(3))], mask, slot, 1 - slot, seed=int(rng.integers(1 << 30)),
+             len_dtype=torch.long if rng.random() < 0.6 else torch.int32, strided=bool(rng.random() < 0.4))
+
+
 @pytest.mark.parametrize("W", [0, 1, 64, 100])
 def test_window_sizes_and_reverse_slots(W):
     g = torch.Generator().manual_seed(W)
