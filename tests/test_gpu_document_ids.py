@@ -63,6 +63,29 @@ def test_against_oracle(t):
     assert np.array_equal(got32.cpu().numpy(), docidx.interleave(want))
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_random_sweep(seed):
+    # Random batch sizes, lengths (across the 1024-token tile boundaries), pad counts, EOS densities,
+    # token and id dtypes and repeat factors: bit-exact against the oracle.
+    rng = np.random.default_rng(7000 + seed)
+    for _ in range(4):
+        b, t = int(rng.integers(1, 6)), int(rng.integers(1, 5000))
+        rows = _random_rows(rng, b, t, max_pads=int(rng.integers(0, t + 1)))
+        if rng.random() < 0.3:  # EOS runs of random density
+            rows[rng.random(rows.shape) < float(rng.uniform(0.0, 0.5))] = EOS
+            for r in range(b):  # keep the rows left padded: no pad after a real token
+                first_real = int(np.argmax(rows[r] != PAD)) if (rows[r] != PAD).any() else t
+                rows[r, first_real:][rows[r, first_real:] == PAD] = 1
+        want = docidx.document_idx(rows, EOS, PAD)
+        tok_dtype = torch.int64 if rng.random() < 0.5 else torch.int32
+        out_dtype = torch.int64 if rng.random() < 0.5 else torch.int32
+        repeat = int(rng.integers(1, 3))
+        got = document_ids(torch.tensor(rows, device="cuda").to(tok_dtype), eos_token_id=EOS, pad_token_id=PAD,
+                           repeat=repeat, dtype=out_dtype)
+        assert got.dtype == out_dtype
+        assert np.array_equal(got.cpu().numpy(), want if repeat == 1 else docidx.interleave(want))
+
+
 def test_strided_rows():
     rng = np.random.default_rng(2)
     rows = _random_rows(rng, 4, 300, max_pads=20)

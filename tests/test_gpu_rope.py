@@ -52,6 +52,26 @@ def test_apply_rotary_emb_matches_oracle(dtype, per_sequence):
     _check(k_out, R.rope(xk.float().numpy(), f.numpy()), dtype)
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_apply_rotary_emb_random_sweep(seed):
+    # Random shapes, head dims (multiples of 8), dtypes and shared or per-sequence frequency tables:
+    # within one output rounding of the float64 oracle.
+    rng = np.random.default_rng(8000 + seed)
+    g = torch.Generator().manual_seed(seed)
+    for _ in range(4):
+        B, T, H = int(rng.integers(1, 4)), int(rng.integers(1, 200)), int(rng.integers(1, 6))
+        D = 8 * int(rng.integers(1, 33))
+        dtype = (torch.bfloat16, torch.float16, torch.float32)[int(rng.integers(3))]
+        xq = torch.randn(B, T, H, D, generator=g).to(dtype)
+        xk = torch.randn(B, T, H, D, generator=g).to(dtype)
+        table = _freqs(D, T + 17)
+        f = table[torch.randint(0, T + 17, (B, T), generator=g)] if rng.random() < 0.5 else table[:T]
+        q_out, k_out = SR.apply_rotary_emb(xq.cuda(), xk.cuda(), f.cuda())
+        torch.cuda.synchronize()
+        _check(q_out, R.rope(xq.float().numpy(), f.numpy()), dtype)
+        _check(k_out, R.rope(xk.float().numpy(), f.numpy()), dtype)
+
+
 @pytest.mark.parametrize("D", [16, 32, 128, 256])
 def test_rope_qkv_from_packed_projection(D):
     # q, k, v as the attention modules split them: views of one [B, T, 3C] projection (fp32).
